@@ -1,0 +1,120 @@
+/*
+ * llmgen_attn.h -- C-ABI of the MI355X (gfx950) attention path for llmgen: libllmgen_attn.so.
+ *
+ * Each entry point replaces one extern of the reference engine's CUDA backend with the same argument list,
+ * meaning, ownership and error behaviour (citations relative to the reference repository root):
+ *   - the three attention launchers: src/backend/cuda/attention/attention_v1.zig:10-48
+ *   - the device context:            src/backend/cuda/cuda_context.zig:1-11, cuda_context.cu:13-126
+ *   - device memory helpers:         src/backend/cuda/memory/memory.zig:1-11
+ * A host that binds `cuda_X` today binds `hip_X` here (see INTEGRATION.md for the Zig stubs).
+ *
+ * Conventions (same as the reference):
+ *   - bf16 tensors are passed as uint16_t bit patterns; index tensors are int32; all pointers are device
+ *     pointers except the host sides of the copy helpers.
+ *   - Every launcher enqueues on the library's one stream (created by hip_init, or the caller's stream after
+ *     hip_set_stream) and returns without synchronising.  Launchers allocate nothing, never synchronise and
+ *     derive grid sizes only from their integer arguments, so they may be called inside graph capture.
+ *   - Launchers return void.  Unsupported shapes print one line to stderr and launch nothing.  Device faults
+ *     surface through hip_last_error() after hip_sync().
+ *   - T <= 0, S <= 0 and n_tiles <= 0 are no-ops.
+ */
+#ifndef LLMGEN_ATTN_H
+#define LLMGEN_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------------------------------------------------
+ * Attention launchers
+ * ------------------------------------------------------------------------------------------------------- */
+
+/* Replaces cuda_store_kv (attention_v1.zig:10; kernel semantics cpu/attention.zig:31-44).
+ * k, v [T, nkv, hd] -> k_cache / v_cache [num_blocks, nkv, block_size, hd] at slot_mapping[t]
+ * (block = slot / block_size, offset = slot % block_size); slot < 0 rows are skipped.  Bit-exact copy.
+ * Accepts any hd that is a multiple of 8 (the reference requires hd == 128 and nkv <= 32). */
+void hip_store_kv(const uint16_t *k, const uint16_t *v, const int32_t *slot_mapping, uint16_t *k_cache,
+                  uint16_t *v_cache, int T, int nkv, int hd, int block_size);
+
+/* Replaces cuda_attn_decode (attention_v1.zig:11-29).  One query token per sequence: q, out [S, nq, hd];
+ * block_tables [S, max_blocks]; ctx_lens [S] = number of cached keys including this step's token.
+ * Split-K scratch is owned by the caller: part_o [S, nq, max_parts, hd] f32 and part_ml [S, nq, max_parts, 2]
+ * f32 (attention_v1.zig:51-57 partSize / maxParts; executor.zig:92-102 sizing).  Part p covers tokens
+ * [p * part_size, (p + 1) * part_size); tokens past max_parts * part_size are not attended (as in the
+ * reference).  ctx <= 0 rows output 0.  Requires hd == 128 and nq / nkv in {1, 2, 4, 8, 16}. */
+void hip_attn_decode(uint16_t *out, const uint16_t *q, const uint16_t *k_cache, const uint16_t *v_cache,
+                     const int32_t *block_tables, const int32_t *ctx_lens, int S, int nq, int nkv, int hd,
+                     int max_blocks, int block_size, float scale, float *part_o, float *part_ml, int part_size,
+                     int max_parts);
+
+/* Replaces cuda_attn_prefill (attention_v1.zig:30-47).  Causal varlen attention over the paged cache: sequence
+ * s owns rows [cu_q[s], cu_q[s+1]) of q / out [T, nq, hd]; ctx_lens[s] = keys after this step; row j sits at
+ * position ctx - q_len + j and attends to keys 0..pos.  Sequences with ctx < q_len are padding: rows of 0.
+ * tile_seq / tile_q0 [n_tiles] list the query tiles of hip_attn_prefill_tile() rows (executor.zig:843-850).
+ * Also used for mixed chunked-prefill + decode steps.  Requires hd == 128 and nq / nkv in {1, 2, 4, 8, 16}
+ * (the reference kernel accepts only 1 and 2). */
+void hip_attn_prefill(uint16_t *out, const uint16_t *q, const uint16_t *k_cache, const uint16_t *v_cache,
+                      const int32_t *block_tables, const int32_t *ctx_lens, const int32_t *cu_q,
+                      const int32_t *tile_seq, const int32_t *tile_q0, int n_tiles, int nq, int nkv, int hd,
+                      int max_blocks, int block_size, float scale);
+
+/* Replaces cuda_attn_prefill_tile (attention_v1.zig:48): query rows per prefill tile (64). */
+int hip_attn_prefill_tile(void);
+
+/* ---------------------------------------------------------------------------------------------------------
+ * Device context (cuda_context.zig:1-11, cuda_context.cu:13-126)
+ * ------------------------------------------------------------------------------------------------------- */
+
+/* Replaces cuda_init: selects device 0 and creates the non-blocking stream.  0 = ok, 1 = no device,
+ * 2 = stream creation failed.  ws_bytes is accepted for signature parity and unused (no library workspace). */
+int hip_init(size_t ws_bytes);
+/* Replaces cuda_sync: waits for the stream. */
+void hip_sync(void);
+/* Replaces cuda_last_error: hipGetLastError(), 0 = no error. */
+int hip_last_error(void);
+/* Replace cuda_graph_begin / _end / _launch / _destroy: capture on the stream (thread-local mode),
+ * end + instantiate (returns a hipGraphExec_t or NULL), replay, destroy. */
+int hip_graph_begin(void);
+void *hip_graph_end(void);
+void hip_graph_launch(void *exec);
+void hip_graph_destroy(void *exec);
+/* Replace cuda_device_count / cuda_mem_info / cuda_device_info (arch receives e.g. 950 for gfx950). */
+int hip_device_count(void);
+void hip_mem_info(size_t *free_mem, size_t *total_mem);
+void hip_device_info(int dev, char *name, int name_cap, size_t *total_mem, int *arch);
+
+/* No reference counterpart: route launches onto a caller-owned stream (e.g. PyTorch's current stream);
+ * NULL selects the legacy default stream.  A stream created by hip_init is destroyed. */
+void hip_set_stream(void *stream);
+void *hip_get_stream(void);
+
+/* ---------------------------------------------------------------------------------------------------------
+ * Memory helpers (memory.zig:1-11)
+ * ------------------------------------------------------------------------------------------------------- */
+void *hip_malloc(size_t bytes);
+void hip_free(void *p);
+void *hip_host_alloc(size_t bytes);
+void hip_host_free(void *p);
+void hip_h2d(void *dst_dev, const void *src_host, size_t bytes);
+void hip_d2h(void *dst_host, const void *src_dev, size_t bytes);
+void hip_d2d(void *dst_dev, const void *src_dev, size_t bytes);
+void hip_h2d_async(void *dst_dev, const void *src_host, size_t bytes);
+void hip_d2h_async(void *dst_host, const void *src_dev, size_t bytes);
+
+/* ---------------------------------------------------------------------------------------------------------
+ * Timing on the launch stream (no reference counterpart; used by the benchmark to time kernels on the
+ * stream they run on)
+ * ------------------------------------------------------------------------------------------------------- */
+void *hip_timer_create(void);
+void hip_timer_record(void *ev);
+float hip_timer_elapsed_ms(void *start, void *stop);
+void hip_timer_destroy(void *ev);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LLMGEN_ATTN_H */

@@ -1,0 +1,72 @@
+"""ctypes binding of libllmgen_attn.so (the C-ABI declared in include/llmgen_attn.h).
+
+The library is loaded from the package directory (built in-tree by ``llmgen_amd.build``).  There is no fallback:
+if the library is missing or fails to load, :func:`lib` raises, so nothing on the product path can silently run
+elsewhere.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+from .build import LIB_PATH
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_F = ctypes.c_float
+_SZ = ctypes.c_size_t
+
+# name -> (restype, argtypes); must match include/llmgen_attn.h
+SIGNATURES = {
+    "hip_store_kv": (None, [_P, _P, _P, _P, _P, _I, _I, _I, _I]),
+    "hip_attn_decode": (None, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P, _P, _I, _I]),
+    "hip_attn_prefill": (None, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F]),
+    "hip_attn_prefill_tile": (_I, []),
+    "hip_init": (_I, [_SZ]),
+    "hip_sync": (None, []),
+    "hip_last_error": (_I, []),
+    "hip_graph_begin": (_I, []),
+    "hip_graph_end": (_P, []),
+    "hip_graph_launch": (None, [_P]),
+    "hip_graph_destroy": (None, [_P]),
+    "hip_device_count": (_I, []),
+    "hip_mem_info": (None, [ctypes.POINTER(_SZ), ctypes.POINTER(_SZ)]),
+    "hip_device_info": (None, [_I, ctypes.c_char_p, _I, ctypes.POINTER(_SZ), ctypes.POINTER(_I)]),
+    "hip_set_stream": (None, [_P]),
+    "hip_get_stream": (_P, []),
+    "hip_malloc": (_P, [_SZ]),
+    "hip_free": (None, [_P]),
+    "hip_host_alloc": (_P, [_SZ]),
+    "hip_host_free": (None, [_P]),
+    "hip_h2d": (None, [_P, _P, _SZ]),
+    "hip_d2h": (None, [_P, _P, _SZ]),
+    "hip_d2d": (None, [_P, _P, _SZ]),
+    "hip_h2d_async": (None, [_P, _P, _SZ]),
+    "hip_d2h_async": (None, [_P, _P, _SZ]),
+    "hip_timer_create": (_P, []),
+    "hip_timer_record": (None, [_P]),
+    "hip_timer_elapsed_ms": (_F, [_P, _P]),
+    "hip_timer_destroy": (None, [_P]),
+}
+
+_lib = None
+
+
+class LibraryMissing(RuntimeError):
+    pass
+
+
+def lib() -> ctypes.CDLL:
+    """Load libllmgen_attn.so (once) and attach the C signatures. Raises LibraryMissing if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise LibraryMissing(f"{LIB_PATH} is not built; run `python -m llmgen_amd.build` (hipcc, gfx950)")
+    handle = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = handle
+    return handle

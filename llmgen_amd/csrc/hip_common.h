@@ -1,0 +1,79 @@
+// hip_common.h -- shared device helpers for the gfx950 attention kernels.
+//
+// Vector types for 16-byte bf16x8 loads, bf16 <-> f32 bit conversions (bf16 is the high half of an f32; the
+// round to bf16 uses the hardware's round-to-nearest-even conversion), wave64 DPP row reductions and the
+// process-global stream every launcher enqueues on.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+
+typedef uint16_t bf16_t;  // bf16 bit pattern as stored in memory
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+// The stream all launchers use; created by hip_init, replaceable with hip_set_stream.
+extern hipStream_t g_llmgen_stream;
+
+#define LLMGEN_LOG2E 1.4426950408889634f
+
+// ---- bf16 <-> f32 ----
+__device__ __forceinline__ float bf16lo_to_f32(uint32_t packed) { return __builtin_bit_cast(float, packed << 16); }
+__device__ __forceinline__ float bf16hi_to_f32(uint32_t packed) {
+    return __builtin_bit_cast(float, packed & 0xFFFF0000u);
+}
+// Unpack 8 bf16 (one 16-byte vector) into f32.
+__device__ __forceinline__ void unpack_bf16x8(const u32x4_t v, float *f) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        f[2 * i] = bf16lo_to_f32(v[i]);
+        f[2 * i + 1] = bf16hi_to_f32(v[i]);
+    }
+}
+// Round two f32 to bf16 (RNE, v_cvt_pk_bf16_f32) and pack lo | hi << 16.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    bf16x2_t r;
+    r[0] = (__bf16)lo;
+    r[1] = (__bf16)hi;
+    return __builtin_bit_cast(uint32_t, r);
+}
+
+// ---- wave64 row (16-lane) reductions through DPP ----
+// DPP controls: quad_perm [1,0,3,2] = 0xB1, quad_perm [2,3,0,1] = 0x4E, row_half_mirror = 0x141,
+// row_mirror = 0x140.  After the two quad steps each quad holds its result; the half-mirror pairs quad 0 with
+// quad 1 (and 2 with 3); the mirror pairs the two halves of the 16-lane row.  All 16 lanes end with the result.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row16_max(float x) {
+    x = fmaxf(x, dpp_f<0xB1>(x));
+    x = fmaxf(x, dpp_f<0x4E>(x));
+    x = fmaxf(x, dpp_f<0x141>(x));
+    x = fmaxf(x, dpp_f<0x140>(x));
+    return x;
+}
+__device__ __forceinline__ float row16_sum(float x) {
+    x += dpp_f<0xB1>(x);
+    x += dpp_f<0x4E>(x);
+    x += dpp_f<0x141>(x);
+    x += dpp_f<0x140>(x);
+    return x;
+}
+
+// Lane exchange across the whole wave (ds_bpermute; no LDS memory is touched).
+__device__ __forceinline__ float lane_xor(float x, int mask) {
+    const int lane = __lane_id();
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, __builtin_bit_cast(int, x)));
+}
+
+// 16-byte global load as four dwords.
+__device__ __forceinline__ u32x4_t ld16(const void *p) { return *reinterpret_cast<const u32x4_t *>(p); }
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

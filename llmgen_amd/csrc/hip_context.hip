@@ -1,0 +1,157 @@
+// hip_context.hip -- device context C-ABI: one process-global stream, memory helpers and stream-capture graphs.
+//
+// Mirrors the reference's device-context boundary (src/backend/cuda/cuda_context.cu:13-126 and
+// src/backend/cuda/memory/memory.zig:1-11): every launcher enqueues on one non-blocking stream, launchers never
+// synchronise, graphs are recorded on that stream in thread-local capture mode.  hip_set_stream and the
+// hip_timer_* helpers have no reference counterpart: the first lets a host that owns its own stream (PyTorch's
+// current stream, for example) route the kernels onto it, the second times work on that same stream.
+#include "hip_common.h"
+
+#include <stdlib.h>
+#include <string.h>
+
+hipStream_t g_llmgen_stream = nullptr;
+static bool g_own_stream = false;
+static hipGraph_t g_capture_graph = nullptr;
+
+#define HIP_WARN(call)                                                                                   \
+    do {                                                                                                 \
+        hipError_t e_ = (call);                                                                          \
+        if (e_ != hipSuccess) fprintf(stderr, "[llmgen-hip] %s failed: %s\n", #call, hipGetErrorString(e_)); \
+    } while (0)
+
+extern "C" {
+
+// cuda_context.cu:13-42.  Creates the global stream on device 0.  ws_bytes is accepted for signature parity
+// (the reference sizes a cuBLAS workspace with it); the attention path needs no library workspace.
+int hip_init(size_t ws_bytes) {
+    (void)ws_bytes;
+    if (g_llmgen_stream) return 0;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) {
+        fprintf(stderr, "[llmgen-hip] no HIP device\n");
+        return 1;
+    }
+    if (hipSetDevice(0) != hipSuccess) return 1;
+    if (hipStreamCreateWithFlags(&g_llmgen_stream, hipStreamNonBlocking) != hipSuccess) {
+        fprintf(stderr, "[llmgen-hip] hipStreamCreateWithFlags failed\n");
+        g_llmgen_stream = nullptr;
+        return 2;
+    }
+    g_own_stream = true;
+    return 0;
+}
+
+// Route all launches onto a stream owned by the caller (nullptr = the legacy default stream).
+void hip_set_stream(void *stream) {
+    if (g_own_stream && g_llmgen_stream) (void)hipStreamDestroy(g_llmgen_stream);
+    g_own_stream = false;
+    g_llmgen_stream = (hipStream_t)stream;
+}
+
+void *hip_get_stream(void) { return (void *)g_llmgen_stream; }
+
+int hip_device_count(void) {
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess) return 0;
+    return count;
+}
+
+// cuda_context.cu:50-64; `arch` receives the gcnArch number (e.g. 950) in place of the CUDA SM version.
+void hip_device_info(int dev, char *name, int name_cap, size_t *total_mem, int *arch) {
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, dev) != hipSuccess) {
+        if (name && name_cap > 0) name[0] = '\0';
+        if (total_mem) *total_mem = 0;
+        if (arch) *arch = 0;
+        return;
+    }
+    if (name && name_cap > 0) {
+        strncpy(name, prop.gcnArchName, name_cap - 1);
+        name[name_cap - 1] = '\0';
+    }
+    if (total_mem) *total_mem = prop.totalGlobalMem;
+    if (arch) *arch = prop.major * 100 + prop.minor * 10;
+}
+
+void hip_mem_info(size_t *free_mem, size_t *total_mem) {
+    if (hipMemGetInfo(free_mem, total_mem) != hipSuccess) {
+        *free_mem = 0;
+        *total_mem = 0;
+    }
+}
+
+// memory.zig:1-11
+void *hip_malloc(size_t bytes) {
+    void *p = nullptr;
+    if (hipMalloc(&p, bytes) != hipSuccess) {
+        fprintf(stderr, "[llmgen-hip] hipMalloc(%zu) failed\n", bytes);
+        return nullptr;
+    }
+    return p;
+}
+void hip_free(void *p) {
+    if (p) HIP_WARN(hipFree(p));
+}
+void *hip_host_alloc(size_t bytes) {
+    void *p = nullptr;
+    if (hipHostMalloc(&p, bytes, hipHostMallocDefault) != hipSuccess) return nullptr;
+    return p;
+}
+void hip_host_free(void *p) {
+    if (p) HIP_WARN(hipHostFree(p));
+}
+void hip_h2d(void *dst, const void *src, size_t n) { HIP_WARN(hipMemcpy(dst, src, n, hipMemcpyHostToDevice)); }
+void hip_d2h(void *dst, const void *src, size_t n) {
+    HIP_WARN(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, g_llmgen_stream));
+    HIP_WARN(hipStreamSynchronize(g_llmgen_stream));
+}
+void hip_d2d(void *dst, const void *src, size_t n) { HIP_WARN(hipMemcpy(dst, src, n, hipMemcpyDeviceToDevice)); }
+void hip_h2d_async(void *dst, const void *src, size_t n) {
+    HIP_WARN(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, g_llmgen_stream));
+}
+void hip_d2h_async(void *dst, const void *src, size_t n) {
+    HIP_WARN(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, g_llmgen_stream));
+}
+
+// cuda_context.cu:96-102.  Launches are asynchronous: errors show up after a sync.
+int hip_last_error(void) { return (int)hipGetLastError(); }
+void hip_sync(void) { HIP_WARN(hipStreamSynchronize(g_llmgen_stream)); }
+
+// cuda_context.cu:106-126.  Graph capture on the global stream.
+int hip_graph_begin(void) { return (int)hipStreamBeginCapture(g_llmgen_stream, hipStreamCaptureModeThreadLocal); }
+void *hip_graph_end(void) {
+    if (hipStreamEndCapture(g_llmgen_stream, &g_capture_graph) != hipSuccess || !g_capture_graph) {
+        fprintf(stderr, "[llmgen-hip] hipStreamEndCapture failed\n");
+        g_capture_graph = nullptr;
+        return nullptr;
+    }
+    hipGraphExec_t exec = nullptr;
+    if (hipGraphInstantiate(&exec, g_capture_graph, nullptr, nullptr, 0) != hipSuccess) exec = nullptr;
+    (void)hipGraphDestroy(g_capture_graph);
+    g_capture_graph = nullptr;
+    return (void *)exec;
+}
+void hip_graph_launch(void *exec) { HIP_WARN(hipGraphLaunch((hipGraphExec_t)exec, g_llmgen_stream)); }
+void hip_graph_destroy(void *exec) {
+    if (exec) (void)hipGraphExecDestroy((hipGraphExec_t)exec);
+}
+
+// ---- timing on the launch stream (measurement helpers; no reference counterpart) ----
+void *hip_timer_create(void) {
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return (void *)e;
+}
+void hip_timer_record(void *ev) { HIP_WARN(hipEventRecord((hipEvent_t)ev, g_llmgen_stream)); }
+float hip_timer_elapsed_ms(void *start, void *stop) {
+    float ms = -1.f;
+    HIP_WARN(hipEventSynchronize((hipEvent_t)stop));
+    HIP_WARN(hipEventElapsedTime(&ms, (hipEvent_t)start, (hipEvent_t)stop));
+    return ms;
+}
+void hip_timer_destroy(void *ev) {
+    if (ev) (void)hipEventDestroy((hipEvent_t)ev);
+}
+
+}  // extern "C"

@@ -1,0 +1,298 @@
+// prefill.hip -- FA2-style causal varlen attention over the paged KV cache on bf16 MFMA (gfx950, wave64).
+//
+// Contract: src/backend/cuda/attention/attention_v1.zig:30-48 (cuda_attn_prefill argument list) with the
+// semantics of src/backend/cpu/attention.zig:64-118: sequence s owns query rows [cu_q[s], cu_q[s+1]) of q
+// [T, nq, 128]; after this step it has ctx[s] keys; query j of the segment sits at position ctx - q_len + j
+// and sees keys 0..pos; output bf16(softmax(scale q K^T) V); a sequence with ctx < q_len is padding and
+// writes zeros.  The host tiles each segment into hip_attn_prefill_tile() rows (tile_seq, tile_q0).
+//
+// Design (one workgroup = one query tile x one KV head x a group of its G query heads):
+//   * each wave owns 32 query rows of one head and computes S^T = K Q^T with v_mfma_f32_32x32x16_bf16: K
+//     (from LDS) is the A operand, Q (registers, loaded once) the B operand.  In the S^T accumulator layout
+//     every lane holds 32 keys of ONE query row, so the online softmax is lane-local except one exchange
+//     between the two half-waves;
+//   * the probabilities are rounded to bf16 in registers and used directly as the B operand of O^T = V^T P^T:
+//     the k-slots of that MFMA are assigned to keys in exactly the order the S^T accumulator holds them.  V^T
+//     comes from LDS, where the loader writes V transposed ([dim][key]) with keys permuted inside each group
+//     of 16 (bits 2 and 3 swapped) so each lane's 8 keys are one 16-byte ds_read;
+//   * K and V tiles of 64 keys are staged through LDS once per workgroup and shared by every wave (all G heads
+//     of the group and both row halves of the tile); the next tile's global loads are issued into registers
+//     before the current tile is computed;
+//   * online softmax in base 2 with scale * log2 e folded in, fp32 row state; causal masking only on tiles
+//     that cross a wave's diagonal; tiles wholly above a wave's diagonal are skipped by that wave;
+//   * grid is 1-D with the KV head fastest, so every workgroup of one KV head lands on the same XCD (8 XCDs,
+//     round-robin dispatch) and its K/V tiles stay in that XCD's L2; heavier (later) query tiles go first.
+#include "hip_common.h"
+
+#include <math.h>
+
+namespace {
+
+constexpr int HD = 128;
+constexpr int BQ = 64;            // query rows per tile (the value hip_attn_prefill_tile returns)
+constexpr int BK = 64;            // keys per LDS tile
+constexpr int KS_STRIDE = HD + 8;  // K tile row stride in bf16 (272 B: rows shift by 4 banks)
+constexpr int VT_STRIDE = BK + 8;  // V^T tile row stride in bf16 (144 B)
+
+__device__ __forceinline__ int swap23(int b) { return (b & ~12) | ((b & 4) << 1) | ((b & 8) >> 1); }
+
+__device__ __forceinline__ long kv_row(const int *__restrict__ bt, int t, int block_size, int bs_shift, long head_off,
+                                       long blk_stride) {
+    const int bi = bs_shift >= 0 ? (t >> bs_shift) : (t / block_size);
+    const int off = t - bi * block_size;
+    return (long)bt[bi] * blk_stride + head_off + (long)off * HD;
+}
+
+// NW = waves per workgroup (2 per head: rows 0-31 and 32-63 of the tile).
+template <int NW>
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)))
+    attn_prefill_kernel(bf16_t *__restrict__ out, const bf16_t *__restrict__ q, const bf16_t *__restrict__ kc,
+                        const bf16_t *__restrict__ vc, const int *__restrict__ block_tables,
+                        const int *__restrict__ ctx_lens, const int *__restrict__ cu_q,
+                        const int *__restrict__ tile_seq, const int *__restrict__ tile_q0, int n_tiles, int nq,
+                        int nkv, int G, int head_groups, int max_blocks, int block_size, int bs_shift,
+                        float scale_log2) {
+    constexpr int NT = 64 * NW;
+    constexpr int K_ITEMS = BK * (HD / 8) / NT;       // 16-byte K chunks per thread per tile
+    constexpr int V_ITEMS = (BK / 2) * (HD / 8) / NT;  // key pairs x 8 dims per thread per tile
+    static_assert(K_ITEMS >= 1 && V_ITEMS >= 1, "tile too small for the workgroup");
+
+    __shared__ __attribute__((aligned(16))) bf16_t Ks[BK * KS_STRIDE];
+    __shared__ __attribute__((aligned(16))) bf16_t Vt[HD * VT_STRIDE];
+
+    const int bid = blockIdx.x;
+    const int kvh = bid % nkv;
+    const int rest = bid / nkv;
+    const int hg = rest % head_groups;
+    const int tile = n_tiles - 1 - rest / head_groups;
+    const int s = tile_seq[tile], q0 = tile_q0[tile];
+    const int q_beg = cu_q[s], q_len = cu_q[s + 1] - q_beg, ctx = ctx_lens[s];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = hg * (NW / 2) + (wave >> 1);  // head within the KV group
+    const int head = kvh * G + g;
+    const int r0 = q0 + (wave & 1) * 32;  // first query row (within the segment) of this wave
+    const int l32 = lane & 31, hh = lane >> 5;
+
+    if (ctx < q_len) {  // padding sequence: zero rows, no keys (cpu/attention.zig:80-83)
+        const int row = r0 + l32;
+        if (row < q_len) {
+            bf16_t *o = out + ((long)(q_beg + row) * nq + head) * HD + hh * 64;
+            for (int d = 0; d < 64; d += 8) *reinterpret_cast<u32x4_t *>(o + d) = u32x4_t{0, 0, 0, 0};
+        }
+        return;
+    }
+
+    const int *bt = block_tables + (long)s * max_blocks;
+    const long blk_stride = (long)nkv * block_size * HD;
+    const long head_off = (long)kvh * block_size * HD;
+    const int base_pos = ctx - q_len;                          // position of segment row 0
+    const int kend = base_pos + min(q0 + BQ, q_len);            // keys needed by the whole tile
+    const int n_iter = (kend + BK - 1) / BK;
+
+    // ---- Q fragments (B operand): lane holds row r0+l32, dims c*16 + hh*8 .. +8 ----
+    const int my_row = r0 + l32;
+    const bool row_valid = my_row < q_len;
+    const int my_pos = base_pos + my_row;
+    bf16x8_t qf[8];
+    {
+        const int rq = min(my_row, q_len - 1);
+        const bf16_t *qp = q + ((long)(q_beg + rq) * nq + head) * HD + hh * 8;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) qf[c] = __builtin_bit_cast(bf16x8_t, ld16(qp + c * 16));
+    }
+    const bool wave_active = r0 < q_len;
+    const int wave_pos_min = base_pos + r0;
+    const int wave_pos_max = base_pos + min(r0 + 31, q_len - 1);
+    const bool wave_has_pad = r0 + 31 >= q_len;
+
+    // ---- global -> register prefetch of one K/V tile ----
+    u32x4_t kreg[K_ITEMS];
+    u32x4_t vreg[V_ITEMS][2];
+    auto prefetch = [&](int it) {
+        const int kb0 = it * BK;
+#pragma unroll
+        for (int i = 0; i < K_ITEMS; ++i) {
+            const int item = tid + i * NT;
+            const int key = min(kb0 + (item >> 4), kend - 1);
+            kreg[i] = ld16(kc + kv_row(bt, key, block_size, bs_shift, head_off, blk_stride) + (item & 15) * 8);
+        }
+#pragma unroll
+        for (int i = 0; i < V_ITEMS; ++i) {
+            const int item = tid + i * NT;
+            const int kp = item & 31, dc = item >> 5;
+            const int k0 = min(kb0 + 2 * kp, kend - 1), k1 = min(kb0 + 2 * kp + 1, kend - 1);
+            vreg[i][0] = ld16(vc + kv_row(bt, k0, block_size, bs_shift, head_off, blk_stride) + dc * 8);
+            vreg[i][1] = ld16(vc + kv_row(bt, k1, block_size, bs_shift, head_off, blk_stride) + dc * 8);
+        }
+    };
+    auto commit = [&]() {
+#pragma unroll
+        for (int i = 0; i < K_ITEMS; ++i) {
+            const int item = tid + i * NT;
+            *reinterpret_cast<u32x4_t *>(Ks + (item >> 4) * KS_STRIDE + (item & 15) * 8) = kreg[i];
+        }
+#pragma unroll
+        for (int i = 0; i < V_ITEMS; ++i) {
+            const int item = tid + i * NT;
+            const int kp = item & 31, dc = item >> 5;
+            const int key0 = 2 * kp;
+            const int pos = (key0 & ~15) | swap23(key0 & 15);
+            bf16_t *dst = Vt + (dc * 8) * VT_STRIDE + pos;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t a = vreg[i][0][j], b = vreg[i][1][j];
+                // dims 2j and 2j+1: (key0, key0+1) pairs of bf16 -> one dword per dim row
+                *reinterpret_cast<uint32_t *>(dst + (2 * j) * VT_STRIDE) = __builtin_amdgcn_perm(b, a, 0x05040100u);
+                *reinterpret_cast<uint32_t *>(dst + (2 * j + 1) * VT_STRIDE) =
+                    __builtin_amdgcn_perm(b, a, 0x07060302u);
+            }
+        }
+    };
+
+    f32x16_t o[4];
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[db][r] = 0.f;
+    float m_run = -INFINITY, l_run = 0.f;
+
+    if (n_iter > 0) prefetch(0);
+    for (int it = 0; it < n_iter; ++it) {
+        const int kb0 = it * BK;
+        __syncthreads();  // every wave is done reading the previous tile
+        commit();
+        __syncthreads();
+        if (it + 1 < n_iter) prefetch(it + 1);
+
+        if (wave_active && kb0 <= wave_pos_max) {
+            // ---- S^T[key][row] = K Q^T: two 32-key blocks x eight 16-dim steps ----
+            f32x16_t sacc[2];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
+                const bf16_t *kp = Ks + (kb * 32 + l32) * KS_STRIDE + hh * 8;
+#pragma unroll
+                for (int c = 0; c < 8; ++c) {
+                    const bf16x8_t a = *reinterpret_cast<const bf16x8_t *>(kp + c * 16);
+                    sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[c], sacc[kb], 0, 0, 0);
+                }
+            }
+            // lane holds row my_row, keys kb0 + kb*32 + (r/4)*8 + hh*4 + r%4
+            const bool need_mask = wave_has_pad || (kb0 + BK - 1 > wave_pos_min);
+            float mx = -INFINITY;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    float v = sacc[kb][r] * scale_log2;
+                    if (need_mask) {
+                        const int key = kb0 + kb * 32 + (r >> 2) * 8 + hh * 4 + (r & 3);
+                        if (!row_valid || key > my_pos) v = -INFINITY;
+                    }
+                    sacc[kb][r] = v;
+                    mx = fmaxf(mx, v);
+                }
+            mx = fmaxf(mx, lane_xor(mx, 32));
+            const float m_new = fmaxf(m_run, mx);
+            const float m_use = m_new == -INFINITY ? 0.f : m_new;
+            const float corr = fast_exp2(m_run - m_use);
+            float lsum = 0.f;
+            bf16x8_t pf[4];  // B fragments for the four 16-key steps of P V
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int half = 0; half < 2; ++half) {
+                    float p[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        p[e] = fast_exp2(sacc[kb][half * 8 + e] - m_use);
+                        lsum += p[e];
+                    }
+                    u32x4_t w;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) w[e] = pack_bf16x2(p[2 * e], p[2 * e + 1]);
+                    pf[kb * 2 + half] = __builtin_bit_cast(bf16x8_t, w);
+                }
+            l_run = l_run * corr + lsum;
+            m_run = m_new;
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[db][r] *= corr;
+            // ---- O^T[dim][row] += V^T P^T ----
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                const bf16_t *vp = Vt + (db * 32 + l32) * VT_STRIDE + hh * 8;
+#pragma unroll
+                for (int kc16 = 0; kc16 < 4; ++kc16) {
+                    const bf16x8_t a = *reinterpret_cast<const bf16x8_t *>(vp + kc16 * 16);
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pf[kc16], o[db], 0, 0, 0);
+                }
+            }
+        }
+    }
+
+    // ---- normalise and store: lane holds dims db*32 + (r/4)*8 + hh*4 + r%4 of row my_row ----
+    if (!wave_active) return;
+    const float l_tot = l_run + lane_xor(l_run, 32);
+    if (!row_valid) return;
+    const float inv = 1.f / l_tot;
+    bf16_t *orow = out + ((long)(q_beg + my_row) * nq + head) * HD + hh * 4;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            u32x2_t w;
+            w[0] = pack_bf16x2(o[db][rr * 4 + 0] * inv, o[db][rr * 4 + 1] * inv);
+            w[1] = pack_bf16x2(o[db][rr * 4 + 2] * inv, o[db][rr * 4 + 3] * inv);
+            *reinterpret_cast<u32x2_t *>(orow + db * 32 + rr * 8) = w;
+        }
+}
+
+template <int NW>
+void launch_prefill(int head_groups, bf16_t *out, const bf16_t *q, const bf16_t *kc, const bf16_t *vc, const int *bt,
+                    const int *ctx, const int *cu_q, const int *tile_seq, const int *tile_q0, int n_tiles, int nq,
+                    int nkv, int G, int max_blocks, int block_size, int bs_shift, float sl2) {
+    const long grid = (long)n_tiles * nkv * head_groups;
+    hipLaunchKernelGGL((attn_prefill_kernel<NW>), dim3((unsigned)grid), dim3(64 * NW), 0, g_llmgen_stream, out, q, kc,
+                       vc, bt, ctx, cu_q, tile_seq, tile_q0, n_tiles, nq, nkv, G, head_groups, max_blocks,
+                       block_size, bs_shift, sl2);
+}
+
+}  // namespace
+
+extern "C" int hip_attn_prefill_tile(void) { return BQ; }
+
+extern "C" void hip_attn_prefill(bf16_t *out, const bf16_t *q, const bf16_t *k_cache, const bf16_t *v_cache,
+                                 const int *block_tables, const int *ctx_lens, const int *cu_q, const int *tile_seq,
+                                 const int *tile_q0, int n_tiles, int nq, int nkv, int hd, int max_blocks,
+                                 int block_size, float scale) {
+    if (n_tiles <= 0) return;
+    if (hd != HD) {
+        fprintf(stderr, "[llmgen-hip] attn_prefill: only head_dim=128 is supported (got %d)\n", hd);
+        return;
+    }
+    if (nkv <= 0 || nq <= 0 || nq % nkv != 0 || block_size <= 0) {
+        fprintf(stderr, "[llmgen-hip] attn_prefill: bad shape nq=%d nkv=%d block_size=%d\n", nq, nkv, block_size);
+        return;
+    }
+    const int G = nq / nkv;
+    if (G != 1 && G != 2 && G != 4 && G != 8 && G != 16) {
+        fprintf(stderr, "[llmgen-hip] attn_prefill: unsupported GQA group size %d\n", G);
+        return;
+    }
+    const int bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz(block_size) : -1;
+    const float sl2 = scale * LLMGEN_LOG2E;
+    // two waves per head; at most 8 waves (4 heads) per workgroup, the rest of the group in further workgroups
+    const int heads_per_wg = G < 4 ? G : 4;
+    const int head_groups = G / heads_per_wg;
+    switch (heads_per_wg) {
+        case 1: launch_prefill<2>(head_groups, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq,
+                                  tile_q0, n_tiles, nq, nkv, G, max_blocks, block_size, bs_shift, sl2); break;
+        case 2: launch_prefill<4>(head_groups, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq,
+                                  tile_q0, n_tiles, nq, nkv, G, max_blocks, block_size, bs_shift, sl2); break;
+        default: launch_prefill<8>(head_groups, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq,
+                                   tile_q0, n_tiles, nq, nkv, G, max_blocks, block_size, bs_shift, sl2); break;
+    }
+}

@@ -1,0 +1,205 @@
+"""Seeded synthetic workloads: the five BASELINE configurations and the reference's own attention test cases.
+
+A :class:`Workload` is one attention step of one layer: the sequences of the step (:class:`~llmgen_amd.step.Entry`
+with a physical block table each), the paged K/V pools as they are before the step (random bf16 history), and
+this step's q / k / v.  The step runs as the engine runs it: store_kv of this step's k / v, then decode or
+prefill attention.  Inputs are drawn N(0,1)*std from a seeded generator and rounded to bf16 (RNE).
+
+Configurations (shape Qwen3-0.6B unless stated: 16 Q heads, 8 KV heads, head_dim 128, block size 256):
+  c1  single-sequence decode, ctx 512, contiguous blocks {0, 1}, std 0.5
+  c2  batched decode, 32 sequences, ctx ~ U[128, 1024], permuted blocks, std 1
+  c3  causal prefill of one 3584-token prompt + 8 prompts of U[128, 512] tokens, std 0.5
+  c4  mixed step: 256 sequences with ctx ~ U[100, 2048]; 8 prefill a 512-token chunk, 248 decode one token
+  c5d decode, 32 Q / 8 KV heads (GQA 4), 16 sequences at ctx 32768, permuted blocks, std 1
+  c5p prefill, 32 Q / 8 KV heads, one 16384-token causal prompt, permuted blocks, std 1
+Reference test cases (src/backend/cuda/kernel_test.zig:151-232, src/backend/cpu/attention.zig:188-251) are
+``kt_prefill``, ``kt_decode`` and ``cpu_mixed``, with U(-1, 1) inputs from a seeded generator.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import List, Optional
+
+import numpy as np
+import torch
+
+from .step import Entry, StepMeta, fill_meta
+
+
+@dataclass
+class Workload:
+    name: str
+    nq: int
+    nkv: int
+    hd: int
+    block_size: int
+    num_blocks: int
+    max_blocks: int
+    max_model_len: int
+    entries: List[Entry]
+    std: float = 1.0
+    uniform: bool = False  # U(-1, 1) instead of N(0, 1) * std
+    seed: int = 0
+    decode: Optional[bool] = None  # None = the engine's rule
+    pad_rows: int = 0  # graph-bucket style padding sequences appended (1 token, ctx = 0, slot = -1)
+    note: str = ""
+
+    @property
+    def scale(self) -> float:
+        return 1.0 / float(np.sqrt(self.hd))
+
+    def meta(self, pf_tile: int) -> StepMeta:
+        return fill_meta(self.entries, self.block_size, self.max_blocks, pf_tile,
+                         seq_num=len(self.entries) + self.pad_rows, decode=self.decode)
+
+    @property
+    def n_tok(self) -> int:
+        return sum(e.q_len for e in self.entries) + self.pad_rows
+
+    @property
+    def ctx_lens(self) -> np.ndarray:
+        return np.array([e.q_start + e.q_len for e in self.entries], np.int64)
+
+    # ---- algorithmic work (the metric definitions) ----
+    def decode_bytes(self) -> int:
+        """K+V bytes of every attended key plus q and out: sum ctx * nkv * hd * 2 B * 2 + 2 * S * nq * hd * 2 B."""
+        ctx = self.ctx_lens
+        return int(ctx.sum()) * self.nkv * self.hd * 2 * 2 + 2 * len(self.entries) * self.nq * self.hd * 2
+
+    def attention_flops(self) -> int:
+        """4 * hd * nq * sum over query rows of the keys it attends (ctx - q_len + j + 1)."""
+        pairs = 0
+        for e in self.entries:
+            ctx, ql = e.q_start + e.q_len, e.q_len
+            # sum_{j<ql} (ctx - ql + j + 1)
+            pairs += ql * (ctx - ql) + ql * (ql + 1) // 2
+        return 4 * self.hd * self.nq * pairs
+
+    def store_kv_bytes(self) -> int:
+        return 2 * 2 * self.n_tok * self.nkv * self.hd * 2  # read + write, K and V
+
+    # ---- tensors ----
+    def tensors(self, device="cpu"):
+        """q [T,nq,hd], k / v [T,nkv,hd] and the pools kc / vc [num_blocks,nkv,bs,hd], all torch.bfloat16 on
+        ``device``.  Deterministic for a given (seed, device type)."""
+        gen = torch.Generator(device=device)
+        gen.manual_seed(self.seed)
+
+        def draw(*shape):
+            if self.uniform:
+                x = torch.rand(*shape, generator=gen, device=device, dtype=torch.float32) * 2 - 1
+            else:
+                x = torch.randn(*shape, generator=gen, device=device, dtype=torch.float32) * self.std
+            return x.to(torch.bfloat16)
+
+        T = self.n_tok
+        pool = (self.num_blocks, self.nkv, self.block_size, self.hd)
+        kc = draw(*pool)
+        vc = draw(*pool)
+        k = draw(T, self.nkv, self.hd)
+        v = draw(T, self.nkv, self.hd)
+        q = draw(T, self.nq, self.hd)
+        return {"q": q, "k": k, "v": v, "kc": kc, "vc": vc}
+
+
+def to_u16(t: torch.Tensor) -> np.ndarray:
+    """bf16 torch tensor -> numpy uint16 bit patterns (host copy)."""
+    return t.detach().contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def _tables(rng: np.random.Generator, ctxs, bs: int, permute: bool, extra_blocks: int = 0):
+    nbs = [(int(c) + bs - 1) // bs for c in ctxs]
+    total = sum(nbs) + extra_blocks
+    ids = rng.permutation(total) if permute else np.arange(total)
+    out, o = [], 0
+    for nb in nbs:
+        out.append([int(x) for x in ids[o:o + nb]])
+        o += nb
+    return out, total
+
+
+def _decode_entries(ctxs, tables):
+    return [Entry(q_start=int(c) - 1, q_len=1, block_table=t) for c, t in zip(ctxs, tables)]
+
+
+def make(name: str, seed: Optional[int] = None) -> Workload:
+    """Build a named workload (see the module docstring)."""
+    bs = 256
+    if name == "c1":
+        s = 1 if seed is None else seed
+        ctxs = [512]
+        tables = [[0, 1]]
+        return Workload("c1", 16, 8, 128, bs, 2, 2, 512, _decode_entries(ctxs, tables), std=0.5, seed=s,
+                        note="decode S=1 ctx=512 contiguous blocks")
+    if name == "c2":
+        s = 2 if seed is None else seed
+        rng = np.random.default_rng(s)
+        ctxs = rng.integers(128, 1025, size=32)
+        tables, nb = _tables(rng, ctxs, bs, permute=True)
+        return Workload("c2", 16, 8, 128, bs, nb, 4, 1024, _decode_entries(ctxs, tables), std=1.0, seed=s,
+                        note="decode S=32 ctx~U[128,1024] permuted blocks")
+    if name == "c3":
+        s = 3 if seed is None else seed
+        rng = np.random.default_rng(s)
+        lens = [3584] + [int(x) for x in rng.integers(128, 513, size=8)]
+        tables, nb = _tables(rng, lens, bs, permute=True)
+        ents = [Entry(0, L, t) for L, t in zip(lens, tables)]
+        return Workload("c3", 16, 8, 128, bs, nb, 14, 4096, ents, std=0.5, seed=s,
+                        note="causal prefill 3584 + 8 x U[128,512]")
+    if name == "c4":
+        s = 4 if seed is None else seed
+        rng = np.random.default_rng(s)
+        n = 256
+        chunk_ids = set(int(x) for x in rng.choice(n, size=8, replace=False))
+        ents_spec = []
+        for i in range(n):
+            if i in chunk_ids:
+                prev = int(rng.integers(100, 2048 - 512 + 1))
+                ents_spec.append((prev, 512))
+            else:
+                ctx = int(rng.integers(100, 2049))
+                ents_spec.append((ctx - 1, 1))
+        ctxs = [a + b for a, b in ents_spec]
+        tables, nb = _tables(rng, ctxs, bs, permute=True)
+        ents = [Entry(a, b, t) for (a, b), t in zip(ents_spec, tables)]
+        return Workload("c4", 16, 8, 128, bs, nb, 8, 2048, ents, std=1.0, seed=s, decode=False,
+                        note="mixed: 8 x 512-token chunks + 248 decodes, ctx~U[100,2048]")
+    if name == "c5d":
+        s = 5 if seed is None else seed
+        rng = np.random.default_rng(s)
+        ctxs = [32768] * 16
+        tables, nb = _tables(rng, ctxs, bs, permute=True)
+        return Workload("c5d", 32, 8, 128, bs, nb, 128, 32768, _decode_entries(ctxs, tables), std=1.0, seed=s,
+                        note="decode GQA4 S=16 ctx=32768 permuted blocks")
+    if name == "c5p":
+        s = 6 if seed is None else seed
+        rng = np.random.default_rng(s)
+        lens = [16384]
+        tables, nb = _tables(rng, lens, bs, permute=True)
+        return Workload("c5p", 32, 8, 128, bs, nb, 64, 32768, [Entry(0, 16384, tables[0])], std=1.0, seed=s,
+                        note="causal prefill GQA4 T=16384 permuted blocks")
+    # ---- reference test cases ----
+    if name in ("kt_prefill", "kt_decode"):
+        # kernel_test.zig:151-232: nq=4, nkv=2, hd=128, bs=16, 32 blocks, ctx=150, bt[i]=(i*7+3)%32 (16 columns)
+        s = 7 if seed is None else seed
+        table = [(i * 7 + 3) % 32 for i in range(16)]
+        if name == "kt_prefill":
+            ents = [Entry(50, 100, table)]  # the last q_len=100 positions of ctx=150 (chunked-prefill tail)
+            return Workload(name, 4, 2, 128, 16, 32, 16, 4096, ents, uniform=True, seed=s,
+                            note="kernel_test prefill: ctx=150, q_len=100")
+        ents = [Entry(149, 1, table)]
+        return Workload(name, 4, 2, 128, 16, 32, 16, 4096, ents, uniform=True, seed=s,
+                        note="kernel_test decode: last row of ctx=150")
+    if name == "cpu_mixed":
+        # cpu/attention.zig:188-251 with head_dim 128 (the kernels' head size): nq=4, nkv=2, bs=16, 24 blocks,
+        # max_blocks=8; seq0 ctx=70 q_len=30, seq1 decode ctx=41, seq2 padding ctx=0
+        s = 11 if seed is None else seed
+        t0 = [(i * 5 + 1) % 24 for i in range(8)]
+        t1 = [(i * 7 + 2) % 24 for i in range(8)]
+        ents = [Entry(40, 30, t0), Entry(40, 1, t1)]
+        return Workload(name, 4, 2, 128, 16, 24, 8, 128, ents, uniform=True, seed=s, decode=False, pad_rows=1,
+                        note="cpu test: chunked tail + decode + padding row")
+    raise KeyError(name)
+
+
+BASELINE_CONFIGS = ("c1", "c2", "c3", "c4", "c5d", "c5p")

@@ -1,0 +1,95 @@
+"""GPU parity: the HIP path (through the C-ABI) against the CPU oracle on the same seeded inputs.
+
+Bars: store_kv bit-exact; attention within max-abs 2e-2 and rel-L2 1e-2 of the oracle's f32 result before bf16
+rounding, and padding rows exactly 0.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from harness import check_hip_error, compare, run_gpu, run_oracle
+from llmgen_amd import attention as A
+from llmgen_amd._lib import lib
+from llmgen_amd.workloads import make, to_u16
+
+pytestmark = pytest.mark.gpu
+
+
+def _sample_rows(wl, meta, n_random=48, seed=0):
+    """First and last row of every prefill tile and sequence, plus seeded random rows."""
+    rows = set()
+    tile = lib().hip_attn_prefill_tile()
+    for s in range(meta.n_seq):
+        b, e = int(meta.cu_q[s]), int(meta.cu_q[s + 1])
+        for q0 in range(b, e, tile):
+            rows.add(q0)
+            rows.add(min(q0 + tile, e) - 1)
+    rng = np.random.default_rng(seed)
+    rows.update(int(x) for x in rng.integers(0, meta.n_tok, size=n_random))
+    return np.array(sorted(rows), np.int32)
+
+
+@pytest.mark.parametrize("name", ["kt_prefill", "cpu_mixed", "c1", "c2"])
+def test_step_matches_oracle_all_rows(gpu, name):
+    wl = make(name)
+    print(f"[gpu-test] {name}", flush=True)
+    t = wl.tensors(device="cuda")
+    out, kc, vc = run_gpu(wl, t)
+    okc, ovc, ob, of = run_oracle(wl, t)
+    assert np.array_equal(to_u16(kc), okc), "store_kv K cache differs"
+    assert np.array_equal(to_u16(vc), ovc), "store_kv V cache differs"
+    got = to_u16(out)
+    compare(got, of, name)
+    # padding rows (ctx < q_len) are exactly zero
+    meta = wl.meta(lib().hip_attn_prefill_tile())
+    for s in range(meta.n_seq):
+        if meta.ctx[s] < meta.cu_q[s + 1] - meta.cu_q[s]:
+            assert not got[meta.cu_q[s]:meta.cu_q[s + 1]].any(), "padding row not zero"
+
+
+@pytest.mark.parametrize("part_size", [64, 128, 256, 512])
+def test_decode_part_size_sweep(gpu, part_size):
+    """kernel_test.zig:212-231: decode of the last row of ctx=150 for several split-K part sizes."""
+    wl = make("kt_decode")
+    print(f"[gpu-test] kt_decode part_size={part_size}", flush=True)
+    t = wl.tensors(device="cuda")
+    _, _, _, of = run_oracle(wl, t)
+    # write this step's K/V through the library, then call the decode launcher directly
+    meta = wl.meta(64)
+    dev = t["q"].device
+    kc, vc = t["kc"].clone(), t["vc"].clone()
+    slots = torch.from_numpy(meta.slots).to(dev)
+    L = lib()
+    L.hip_store_kv(t["k"].data_ptr(), t["v"].data_ptr(), slots.data_ptr(), kc.data_ptr(), vc.data_ptr(), 1, wl.nkv,
+                   wl.hd, wl.block_size)
+    max_parts = (4096 + part_size - 1) // part_size
+    po = torch.empty(wl.nq * max_parts * wl.hd, dtype=torch.float32, device=dev)
+    pml = torch.empty(wl.nq * max_parts * 2, dtype=torch.float32, device=dev)
+    bt = torch.from_numpy(meta.block_tables).to(dev)
+    ctx = torch.from_numpy(meta.ctx).to(dev)
+    out = torch.full((1, wl.nq, wl.hd), float("nan"), dtype=torch.bfloat16, device=dev)
+    L.hip_attn_decode(out.data_ptr(), t["q"].data_ptr(), kc.data_ptr(), vc.data_ptr(), bt.data_ptr(),
+                      ctx.data_ptr(), 1, wl.nq, wl.nkv, wl.hd, wl.max_blocks, wl.block_size, wl.scale,
+                      po.data_ptr(), pml.data_ptr(), part_size, max_parts)
+    torch.cuda.synchronize()
+    check_hip_error("decode")
+    compare(to_u16(out), of, f"kt_decode ps={part_size}")
+
+
+@pytest.mark.parametrize("name", ["c3", "c4"])
+def test_step_matches_oracle_sampled_rows(gpu, name):
+    wl = make(name)
+    print(f"[gpu-test] {name}", flush=True)
+    t = wl.tensors(device="cuda")
+    out, kc, vc = run_gpu(wl, t)
+    meta = wl.meta(lib().hip_attn_prefill_tile())
+    rows = _sample_rows(wl, meta)
+    okc, ovc, ob, of = run_oracle(wl, t, rows=rows, threads=16)
+    assert np.array_equal(to_u16(kc), okc), "store_kv K cache differs"
+    assert np.array_equal(to_u16(vc), ovc), "store_kv V cache differs"
+    compare(to_u16(out)[rows], of, name)
