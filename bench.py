@@ -1,0 +1,269 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X attention path on BASELINE's configurations (1 GPU).
+
+A step is one layer's attention step of configuration c2 (32-sequence batched decode, the configuration the
+metric is quoted on): store_kv of the step's K/V plus split-K paged decode, replayed from a hipGraph decode
+bucket as the engine replays it.  ``value`` = algorithmic decode bytes (sum ctx * nkv * hd * 2 B * 2 + q + out)
+per step / step time, in GB/s.  The other configurations are reported under ``extra``: decode GB/s for c1 and
+c5d, prefill TFLOP/s (4 * hd * nq * causal pairs / time) for c3 and c5p, and the mixed step c4.
+
+All timings use HIP events recorded on the stream the kernels run on.  ``roofline`` is for the dominant kernel
+launch (hip_attn_decode on c2).  ``cpu_baseline`` times the CPU oracle (a C restatement of the reference CPU
+backend's attention, single-threaded like the reference) on a bounded sample of the same workload.
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--no-extra] [--only c2|c5d|c3|...]
+"""
+from __future__ import annotations
+
+import argparse
+import copy
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+ROOT = os.path.dirname(os.path.abspath(__file__))
+
+
+def _timer_pair():
+    from llmgen_amd._lib import lib
+
+    L = lib()
+    return L.hip_timer_create(), L.hip_timer_create()
+
+
+def time_launches(fn, iters: int, warmup: int) -> float:
+    """Average ms per call of fn() over ``iters`` back-to-back calls, HIP events on the launch stream."""
+    import torch
+    from llmgen_amd._lib import lib
+
+    L = lib()
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = _timer_pair()
+    L.hip_timer_record(e0)
+    for _ in range(iters):
+        fn()
+    L.hip_timer_record(e1)
+    ms = L.hip_timer_elapsed_ms(e0, e1)
+    torch.cuda.synchronize()
+    L.hip_timer_destroy(e0)
+    L.hip_timer_destroy(e1)
+    return ms / iters
+
+
+class Step:
+    """One workload's attention step wired to the library (eager launchers + optional decode graph)."""
+
+    def __init__(self, name: str):
+        import torch
+        from llmgen_amd import attention as A
+        from llmgen_amd._lib import lib
+        from llmgen_amd.workloads import make
+
+        self.L = lib()
+        self.wl = wl = make(name)
+        self.t = wl.tensors(device="cuda")
+        self.meta = wl.meta(self.L.hip_attn_prefill_tile())
+        self.ws = A.Workspace.allocate(wl.nq, wl.hd, self.meta.n_seq, wl.max_model_len,
+                                       meta_elems=self.meta.packed().size)
+        self.layer = A.LayerState(self.t["kc"].clone(), self.t["vc"].clone())
+        mgr = A.PagedAttentionManager()
+        mgr.layers[0] = self.layer
+        A.g_attn_mgr = mgr
+        # a private copy: later bind_step calls (graph capture) rewrite the global g_step
+        self.g = copy.copy(A.bind_step(self.meta, self.ws, wl.nq, wl.nkv, wl.hd, wl.block_size, wl.max_blocks,
+                                       wl.max_model_len))
+        self.out = torch.zeros(wl.n_tok, wl.nq, wl.hd, dtype=torch.bfloat16, device="cuda")
+        self.node = A.AttnNode(self.out, [self.t["q"], self.t["k"], self.t["v"]], layer_id=0)
+        self.A = A
+        # write this step's K/V once so attention-only launches see the full context
+        self.store_kv()
+        torch.cuda.synchronize()
+
+    def store_kv(self):
+        g, wl = self.g, self.wl
+        self.L.hip_store_kv(self.t["k"].data_ptr(), self.t["v"].data_ptr(), g.slots, self.layer.k.data_ptr(),
+                            self.layer.v.data_ptr(), g.n_tok, wl.nkv, wl.hd, wl.block_size)
+
+    def attn(self):
+        """The attention launcher alone (decode or prefill), as PagedAttentionImpl issues it after store_kv."""
+        from llmgen_amd import step as S
+
+        g, wl = self.g, self.wl
+        if g.decode:
+            self.L.hip_attn_decode(self.out.data_ptr(), self.t["q"].data_ptr(), self.layer.k.data_ptr(),
+                                   self.layer.v.data_ptr(), g.block_tables, g.ctx, g.n_seq, wl.nq, wl.nkv, wl.hd,
+                                   wl.max_blocks, wl.block_size, g.attn_scale, g.part_o, g.part_ml,
+                                   S.part_size(g.n_seq), S.max_parts(g.n_seq, wl.max_model_len))
+        else:
+            self.L.hip_attn_prefill(self.out.data_ptr(), self.t["q"].data_ptr(), self.layer.k.data_ptr(),
+                                    self.layer.v.data_ptr(), g.block_tables, g.ctx, g.cu_q, g.tile_seq, g.tile_q0,
+                                    g.n_tiles, wl.nq, wl.nkv, wl.hd, wl.max_blocks, wl.block_size, g.attn_scale)
+
+    def full_step(self):
+        self.A.PagedAttentionImpl.execute(0, self.node)
+
+
+def bench_extra(name: str, iters: int) -> dict:
+    st = Step(name)
+    wl = st.wl
+    ms = time_launches(st.attn, iters, warmup=2)
+    ms_kv = time_launches(st.store_kv, iters, warmup=1)
+    r = {"config": name, "note": wl.note, "attn_us": round(ms * 1e3, 2), "store_kv_us": round(ms_kv * 1e3, 2),
+         "store_kv_GBs": round(wl.store_kv_bytes() / (ms_kv * 1e-3) / 1e9, 1)}
+    if st.meta.decode:
+        gbs = wl.decode_bytes() / (ms * 1e-3) / 1e9
+        r.update(decode_GBs=round(gbs, 1), hbm_frac=round(gbs / HBM_PEAK_GBS, 4))
+    else:
+        tf = wl.attention_flops() / (ms * 1e-3) / 1e12
+        gbs = wl.decode_bytes() / (ms * 1e-3) / 1e9
+        r.update(prefill_TFLOPs=round(tf, 1), mfma_frac=round(tf / BF16_PEAK_TFLOPS, 4), kv_GBs=round(gbs, 1))
+    return r
+
+
+def cpu_baseline(st: "Step", budget_s: float = 10.0) -> dict:
+    """The CPU oracle (single thread, like the reference's scalar loop) on full c2 steps, repeated until
+    ``budget_s`` seconds of CPU work; value in the metric's unit (GB/s of algorithmic decode bytes)."""
+    sys.path.insert(0, ROOT)
+    import oracle
+    from llmgen_amd.workloads import to_u16
+
+    wl, meta = st.wl, st.meta
+    q = to_u16(st.t["q"])
+    kc = to_u16(st.layer.k)
+    vc = to_u16(st.layer.v)
+    args = (q, kc, vc, meta.block_tables, meta.ctx, meta.cu_q, wl.nq, wl.nkv, wl.hd, wl.max_blocks, wl.block_size,
+            wl.scale)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        ob, of = oracle.attend(*args)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    per = el / reps
+    # parity of the GPU output of the same step (already computed by the benchmark's warm-up)
+    got = oracle.bf16_to_f32(to_u16(st.out)).astype(np.float64)
+    err = float(np.abs(got - of).max())
+    rel = float(np.linalg.norm(got - of) / np.linalg.norm(of))
+    return {
+        "value": round(wl.decode_bytes() / per / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+        "sample": f"full c2 decode step (32 seqs, all heads) x{reps} reps, {per * 1e3:.1f} ms/step, oracle/attend",
+        "gpu_vs_oracle": {"max_abs": round(err, 5), "rel_l2": round(rel, 5)},
+    }
+
+
+def load_traffic(kernel_key: str):
+    p = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(p):
+        return None
+    with open(p) as f:
+        d = json.load(f)
+    v = d.get(kernel_key)
+    return None if v is None else v.get("hbm_bytes_per_launch")
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--only", default=None, help="time only this config's attention launcher (for profiling)")
+    ap.add_argument("--copy-mb", type=int, default=0,
+                    help="run only a plain device copy of this many MiB (calibrates rocprofv3 FETCH/WRITE_SIZE)")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (the attention kernel on one GPU's share); "
+              f"--gpus {args.gpus} is not supported", file=sys.stderr)
+        return 2
+
+    import torch
+    from llmgen_amd.attention import init_device
+
+    init_device()
+
+    if args.copy_mb:
+        n = args.copy_mb << 20
+        src = torch.ones(n // 4, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": n, "launches": args.steps}), flush=True)
+        return 0
+
+    if args.only:
+        st = Step(args.only)
+        ms = time_launches(st.attn, args.steps, args.warmup)
+        print(json.dumps({"config": args.only, "attn_us": round(ms * 1e3, 2)}), flush=True)
+        return 0
+
+    # ---- the metric step: c2 decode, store_kv + decode replayed from a hipGraph bucket ----
+    from llmgen_amd.graphs import DecodeGraphs
+
+    st = Step("c2")
+    wl = st.wl
+    graphs = DecodeGraphs(st.layer, wl.nq, wl.nkv, wl.hd, wl.block_size, wl.max_blocks, wl.max_model_len,
+                          max_seqs=len(wl.entries), buckets=[len(wl.entries)])
+    b = graphs.prepare(wl.entries, st.t["q"], st.t["k"], st.t["v"])
+    for _ in range(args.warmup):
+        graphs.launch(b)
+    torch.cuda.synchronize()
+    L = st.L
+    e0, e1 = _timer_pair()
+    torch.cuda.synchronize()  # barrier (one rank) + synchronize
+    L.hip_timer_record(e0)
+    for _ in range(args.steps):
+        graphs.launch(b)
+    L.hip_timer_record(e1)
+    step_ms = L.hip_timer_elapsed_ms(e0, e1) / args.steps
+    torch.cuda.synchronize()
+    st.out.copy_(b.out[: len(wl.entries)])
+    value = wl.decode_bytes() / (step_ms * 1e-3) / 1e9
+
+    # ---- dominant kernel launch: hip_attn_decode alone (split-K partials + merge), events on its stream ----
+    kern_ms = time_launches(st.attn, max(args.steps, 50), warmup=3)
+    achieved = wl.decode_bytes() / (kern_ms * 1e-3) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic("decode_c2"),
+                "kernel": "hip_attn_decode (attn_decode_split_kernel + attn_decode_reduce_kernel)",
+                "launch_us": round(kern_ms * 1e3, 2), "bytes_per_launch": wl.decode_bytes()}
+
+    extra = {}
+    if not args.no_extra:
+        for name in ("c1", "c5d", "c3", "c5p", "c4"):
+            try:
+                extra[name] = bench_extra(name, iters=20 if name != "c5p" else 5)
+            except Exception as e:  # report, keep the headline line
+                extra[name] = {"error": repr(e)}
+            torch.cuda.empty_cache()
+
+    line = {
+        "metric": "decode attn HBM GB/s (% of peak) + prefill attn TFLOP/s (% MFMA peak), 1 GPU",
+        "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (seeded N(0,1) bf16 q/k/v and KV history, random block tables)",
+        "config": {"workload": "c2: batched decode, 32 seqs, ctx~U[128,1024], 16q/8kv/hd128, block 256, "
+                               "store_kv + split-K decode replayed from a hipGraph bucket",
+                   "hbm_frac": round(value / HBM_PEAK_GBS, 4), "parallelism": "single GPU"},
+        "roofline": roofline,
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(st)
+    line["extra"] = extra
+    graphs.destroy()
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
