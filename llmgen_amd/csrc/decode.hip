@@ -30,29 +30,32 @@ constexpr int HD = 128;
 constexpr int DEC_WAVES = 4;
 constexpr int DEC_THREADS = 64 * DEC_WAVES;
 
-// Physical row offset (in elements) of logical token t of one sequence, for KV head kvh.
-__device__ __forceinline__ long kv_row(const int *__restrict__ bt, int t, int block_size, int bs_shift, long head_off,
-                                       long blk_stride) {
-    const int bi = bs_shift >= 0 ? (t >> bs_shift) : (t / block_size);
-    const int off = t - bi * block_size;
-    return (long)bt[bi] * blk_stride + head_off + (long)off * HD;
+// Block-table lookup of logical token t (POW2: block_size == 1 << bs_shift).
+template <bool POW2>
+__device__ __forceinline__ int blk_index(int t, int block_size, int bs_shift) {
+    return POW2 ? (t >> bs_shift) : (t / block_size);
 }
 
-// G = query heads per KV head (1..16); NT = 16-token tiles per wave per round.
-template <int G, int NT>
+// G = query heads per KV head (1..16); NT = 16-token tiles per wave per round (a round is 4 waves x 16*NT
+// tokens).  Each workgroup streams `span` tokens of one (kv head, sequence) pair: round r+1's block-table and
+// K/V loads are issued before round r is computed (register double buffering), so every wave keeps one round
+// of loads in flight while it computes.
+template <int G, int NT, bool POW2>
 __global__ void __launch_bounds__(DEC_THREADS)
     attn_decode_split_kernel(bf16_t *__restrict__ out, float *__restrict__ part_o, float *__restrict__ part_ml,
                              const bf16_t *__restrict__ q, const bf16_t *__restrict__ kc,
                              const bf16_t *__restrict__ vc, const int *__restrict__ block_tables,
                              const int *__restrict__ ctx_lens, int nq, int nkv, int max_blocks, int block_size,
-                             int bs_shift, float scale_log2, int part_size, int max_parts, int rounds) {
-    constexpr int WTOK = NT * 16;      // tokens per wave per round
+                             int bs_shift, float scale_log2, int span, int max_parts) {
+    constexpr int WTOK = NT * 16;              // tokens per wave per round
+    constexpr int RTOK = DEC_WAVES * WTOK;     // tokens per round
     const int kvh = blockIdx.x, s = blockIdx.y, part = blockIdx.z;
     const int ctx = ctx_lens[s];
-    const int t0 = part * part_size;
+    const int t0 = part * span;
     if (t0 >= ctx) return;
-    const int n = min(ctx - t0, part_size);
-    const int np = (ctx + part_size - 1) / part_size;
+    const int n = min(ctx - t0, span);
+    const int np = (ctx + span - 1) / span;
+    const int rounds = (n + RTOK - 1) / RTOK;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 15, rgrp = lane >> 4;
 
@@ -64,7 +67,8 @@ __global__ void __launch_bounds__(DEC_THREADS)
 
     const int *bt = block_tables + (long)s * max_blocks;
     const long blk_stride = (long)nkv * block_size * HD;
-    const long head_off = (long)kvh * block_size * HD;
+    const bf16_t *kbase = kc + (long)kvh * block_size * HD;
+    const bf16_t *vbase = vc + (long)kvh * block_size * HD;
 
     // A operand: row g = col holds head kvh*G+g; lane group rgrp holds dims c*32 + rgrp*8 .. +8 of chunk c.
     bf16x8_t qa[4];
@@ -90,25 +94,51 @@ __global__ void __launch_bounds__(DEC_THREADS)
 #pragma unroll
         for (int k = 0; k < 8; ++k) o[g][k] = 0.f;
 
-    for (int r = 0; r < rounds; ++r) {
-        const int wbase = r * DEC_WAVES * WTOK + wave * WTOK;  // first token (within the part) of this wave
-
-        // ---- issue every K and V load of the round ----
+    // K: tile tau, chunk c = dims c*32 + rgrp*8 of token col; V: token rgrp + 4j, dims col*8.
+    struct Buf {
         u32x4_t kf[NT][4];
+        u32x4_t vf[4 * NT];
+    };
+    auto load = [&](int r, Buf &b) {
+        const int wbase = r * RTOK + wave * WTOK;
+        int kt[NT], vt[4 * NT], kblk[NT], vblk[4 * NT];
+#pragma unroll
+        for (int tau = 0; tau < NT; ++tau) kt[tau] = t0 + min(wbase + tau * 16 + col, n - 1);
+#pragma unroll
+        for (int j = 0; j < 4 * NT; ++j) vt[j] = t0 + min(wbase + rgrp + 4 * j, n - 1);
+        if (POW2 && block_size >= WTOK) {
+            // the wave's WTOK tokens touch at most two blocks: two scalar block-table reads (scalar cache,
+            // their own wait counter), then a per-lane select
+            const int b0 = __builtin_amdgcn_readfirstlane((t0 + min(wbase, n - 1)) >> bs_shift);
+            const int b1 = __builtin_amdgcn_readfirstlane((t0 + min(wbase + WTOK - 1, n - 1)) >> bs_shift);
+            const int p0 = bt[b0], p1 = bt[b1];
+#pragma unroll
+            for (int tau = 0; tau < NT; ++tau) kblk[tau] = (kt[tau] >> bs_shift) == b0 ? p0 : p1;
+#pragma unroll
+            for (int j = 0; j < 4 * NT; ++j) vblk[j] = (vt[j] >> bs_shift) == b0 ? p0 : p1;
+        } else {
+            // all block-table reads first (independent), then all K/V reads
+#pragma unroll
+            for (int tau = 0; tau < NT; ++tau) kblk[tau] = bt[blk_index<POW2>(kt[tau], block_size, bs_shift)];
+#pragma unroll
+            for (int j = 0; j < 4 * NT; ++j) vblk[j] = bt[blk_index<POW2>(vt[j], block_size, bs_shift)];
+        }
 #pragma unroll
         for (int tau = 0; tau < NT; ++tau) {
-            const int i = min(wbase + tau * 16 + col, n - 1);  // clamp: masked later, address stays valid
-            const bf16_t *kr = kc + kv_row(bt, t0 + i, block_size, bs_shift, head_off, blk_stride) + rgrp * 8;
+            const int off = kt[tau] - blk_index<POW2>(kt[tau], block_size, bs_shift) * block_size;
+            const bf16_t *kr = kbase + (long)kblk[tau] * blk_stride + (long)off * HD + rgrp * 8;
 #pragma unroll
-            for (int c = 0; c < 4; ++c) kf[tau][c] = ld16(kr + c * 32);
+            for (int c = 0; c < 4; ++c) b.kf[tau][c] = ld16(kr + c * 32);
         }
-        u32x4_t vf[4 * NT];
 #pragma unroll
         for (int j = 0; j < 4 * NT; ++j) {
-            const int i = min(wbase + rgrp + 4 * j, n - 1);
-            vf[j] = ld16(vc + kv_row(bt, t0 + i, block_size, bs_shift, head_off, blk_stride) + col * 8);
+            const int off = vt[j] - blk_index<POW2>(vt[j], block_size, bs_shift) * block_size;
+            b.vf[j] = ld16(vbase + (long)vblk[j] * blk_stride + (long)off * HD + col * 8);
         }
+    };
 
+    auto compute = [&](int r, const Buf &b) {
+        const int wbase = r * RTOK + wave * WTOK;
         // ---- scores on the matrix cores: D[g][token] = sum_d q[g][d] k[token][d] ----
         f32x4_t sc[NT];
 #pragma unroll
@@ -116,15 +146,14 @@ __global__ void __launch_bounds__(DEC_THREADS)
             f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int c = 0; c < 4; ++c)
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[c], __builtin_bit_cast(bf16x8_t, kf[tau][c]), acc,
-                                                              0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[c], __builtin_bit_cast(bf16x8_t, b.kf[tau][c]),
+                                                              acc, 0, 0, 0);
             const bool valid = wbase + tau * 16 + col < n;
 #pragma unroll
             for (int i = 0; i < 4; ++i) sc[tau][i] = valid ? acc[i] * scale_log2 : -INFINITY;
         }
-
-        // ---- online softmax for this round (row rgrp*4+i of the MFMA output = head g; rows past G hold the
-        //      zero query rows and are computed but never stored) ----
+        // ---- online softmax (row rgrp*4+i of the MFMA output = head g; rows past G hold the zero query
+        //      rows and are computed but never stored) ----
         float corr[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -145,6 +174,7 @@ __global__ void __launch_bounds__(DEC_THREADS)
             l_run[i] = l_run[i] * corr[i] + sum;
             m_run[i] = m_new;
         }
+        // probabilities to this wave's LDS slice (wave-private: a wavefront fence orders write -> read)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int g = rgrp * 4 + i;
@@ -154,8 +184,9 @@ __global__ void __launch_bounds__(DEC_THREADS)
                 if (col == 0) corr_lds[wave][g] = corr[i];
             }
         }
-        __syncthreads();
-
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         // ---- P V on the vector ALUs: lane holds dims col*8.. of tokens rgrp + 4j ----
         float cr[G];
 #pragma unroll
@@ -167,7 +198,7 @@ __global__ void __launch_bounds__(DEC_THREADS)
 #pragma unroll
         for (int j = 0; j < 4 * NT; ++j) {
             float f[8];
-            unpack_bf16x8(vf[j], f);
+            unpack_bf16x8(b.vf[j], f);
             const float *pp = p_lds[wave][rgrp + 4 * j];
 #pragma unroll
             for (int g = 0; g < G; ++g) {
@@ -176,7 +207,20 @@ __global__ void __launch_bounds__(DEC_THREADS)
                 for (int k = 0; k < 8; ++k) o[g][k] += p * f[k];
             }
         }
-        __syncthreads();  // p_lds / corr_lds are rewritten next round
+        // the next round rewrites p_lds: keep every lane's reads ahead of those writes
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+
+    Buf bufA, bufB;
+    load(0, bufA);
+    for (int r = 0; r < rounds; r += 2) {
+        if (r + 1 < rounds) load(r + 1, bufB);
+        compute(r, bufA);
+        if (r + 1 >= rounds) break;
+        if (r + 2 < rounds) load(r + 2, bufA);
+        compute(r + 1, bufB);
     }
 
     // ---- per-wave totals ----
@@ -237,61 +281,74 @@ __global__ void __launch_bounds__(DEC_THREADS)
 }
 
 // attention.cu:186-207 semantics: out = sum_p 2^(m_p - M) o_p / sum_p 2^(m_p - M) l_p (m in base 2 here).
-__global__ void __launch_bounds__(HD) attn_decode_reduce_kernel(bf16_t *__restrict__ out,
-                                                                const float *__restrict__ part_o,
-                                                                const float *__restrict__ part_ml,
-                                                                const int *__restrict__ ctx_lens, int nq,
-                                                                int part_size, int max_parts) {
-    const int h = blockIdx.x, s = blockIdx.y, d = threadIdx.x;
+// One workgroup per (kv head, sequence) covers the G heads of the group; a sequence whose context fits one span
+// was finished by the split kernel.
+__global__ void __launch_bounds__(DEC_THREADS) attn_decode_reduce_kernel(bf16_t *__restrict__ out,
+                                                                        const float *__restrict__ part_o,
+                                                                        const float *__restrict__ part_ml,
+                                                                        const int *__restrict__ ctx_lens, int nq,
+                                                                        int G, int span, int nparts, int max_parts) {
+    const int kvh = blockIdx.x, s = blockIdx.y;
     const int ctx = ctx_lens[s];
-    bf16_t *o = out + ((long)s * nq + h) * HD;
-    if (ctx <= 0) {
-        o[d] = 0;
-        return;
+    if (ctx > 0 && (ctx + span - 1) / span == 1) return;
+    const int np = ctx > 0 ? min((ctx + span - 1) / span, nparts) : 0;
+    for (int idx = threadIdx.x; idx < G * HD; idx += DEC_THREADS) {
+        const int g = idx / HD, d = idx % HD;
+        const long h = (long)kvh * G + g;
+        bf16_t *o = out + ((long)s * nq + h) * HD + d;
+        if (np == 0) {
+            *o = 0;
+            continue;
+        }
+        const float *ml = part_ml + ((long)s * nq + h) * max_parts * 2;
+        const float *po = part_o + ((long)s * nq + h) * max_parts * HD + d;
+        float M = -INFINITY;
+        for (int p = 0; p < np; ++p) M = fmaxf(M, ml[2 * p]);
+        float num = 0.f, den = 0.f;
+#pragma unroll 4
+        for (int p = 0; p < np; ++p) {
+            const float w = fast_exp2(ml[2 * p] - M);
+            num += w * po[(long)p * HD];
+            den += w * ml[2 * p + 1];
+        }
+        *o = __builtin_bit_cast(bf16_t, (__bf16)(num / den));
     }
-    int np = (ctx + part_size - 1) / part_size;
-    if (np == 1) return;  // the split kernel wrote the final row
-    np = min(np, max_parts);
-    const float *ml = part_ml + ((long)s * nq + h) * max_parts * 2;
-    const float *po = part_o + ((long)s * nq + h) * max_parts * HD;
-    float M = -INFINITY;
-    for (int p = 0; p < np; ++p) M = fmaxf(M, ml[2 * p]);
-    float num = 0.f, den = 0.f;
-    for (int p = 0; p < np; ++p) {
-        const float w = fast_exp2(ml[2 * p] - M);
-        num += w * po[(long)p * HD + d];
-        den += w * ml[2 * p + 1];
-    }
-    o[d] = __builtin_bit_cast(bf16_t, (__bf16)(num / den));
+}
+
+struct DecodeArgs {
+    bf16_t *out;
+    const bf16_t *q, *kc, *vc;
+    const int *bt, *ctx;
+    int nq, nkv, max_blocks, block_size, bs_shift;
+    float sl2;
+    float *part_o, *part_ml;
+    int span, max_parts;
+};
+
+template <int G, int NT, bool POW2>
+void launch_split(dim3 grid, const DecodeArgs &a) {
+    hipLaunchKernelGGL((attn_decode_split_kernel<G, NT, POW2>), grid, dim3(DEC_THREADS), 0, g_llmgen_stream, a.out,
+                       a.part_o, a.part_ml, a.q, a.kc, a.vc, a.bt, a.ctx, a.nq, a.nkv, a.max_blocks, a.block_size,
+                       a.bs_shift, a.sl2, a.span, a.max_parts);
 }
 
 template <int G, int NT>
-void launch_split(dim3 grid, bf16_t *out, const bf16_t *q, const bf16_t *kc, const bf16_t *vc, const int *bt,
-                  const int *ctx, int nq, int nkv, int max_blocks, int block_size, int bs_shift, float sl2,
-                  float *part_o, float *part_ml, int part_size, int max_parts, int rounds) {
-    hipLaunchKernelGGL((attn_decode_split_kernel<G, NT>), grid, dim3(DEC_THREADS), 0, g_llmgen_stream, out, part_o,
-                       part_ml, q, kc, vc, bt, ctx, nq, nkv, max_blocks, block_size, bs_shift, sl2, part_size,
-                       max_parts, rounds);
+void launch_pow2(dim3 grid, const DecodeArgs &a) {
+    if (a.bs_shift >= 0)
+        launch_split<G, NT, true>(grid, a);
+    else
+        launch_split<G, NT, false>(grid, a);
 }
 
-template <int G>
-bool dispatch_nt(int nt, dim3 grid, bf16_t *out, const bf16_t *q, const bf16_t *kc, const bf16_t *vc, const int *bt,
-                 const int *ctx, int nq, int nkv, int max_blocks, int block_size, int bs_shift, float sl2,
-                 float *part_o, float *part_ml, int part_size, int max_parts, int rounds) {
-#define LLMGEN_NT(N)                                                                                              \
-    case N:                                                                                                       \
-        launch_split<G, N>(grid, out, q, kc, vc, bt, ctx, nq, nkv, max_blocks, block_size, bs_shift, sl2, part_o, \
-                           part_ml, part_size, max_parts, rounds);                                                \
-        return true;
-    switch (nt) {
-        LLMGEN_NT(1)
-        LLMGEN_NT(2)
-        LLMGEN_NT(3)
-        LLMGEN_NT(4)
-        default:
-            return false;
+int num_compute_units() {
+    static int n = 0;
+    if (n == 0) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
     }
-#undef LLMGEN_NT
+    return n;
 }
 
 }  // namespace
@@ -311,32 +368,28 @@ extern "C" void hip_attn_decode(bf16_t *out, const bf16_t *q, const bf16_t *k_ca
         return;
     }
     const int G = nq / nkv;
-    const int nt_cap = G <= 4 ? 4 : (G == 8 ? 2 : 1);  // register budget: o holds G*8 floats per lane
-    int nt = (part_size + 63) / 64;
-    if (nt > nt_cap) nt = nt_cap;
-    const int per_round = DEC_WAVES * 16 * nt;
-    const int rounds = (part_size + per_round - 1) / per_round;
-    const int bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz(block_size) : -1;
-    const float sl2 = scale * LLMGEN_LOG2E;
-    const dim3 grid(nkv, S, max_parts);
-    bool ok = false;
-    switch (G) {
-        case 1: ok = dispatch_nt<1>(nt, grid, out, q, k_cache, v_cache, block_tables, ctx_lens, nq, nkv, max_blocks,
-                                    block_size, bs_shift, sl2, part_o, part_ml, part_size, max_parts, rounds); break;
-        case 2: ok = dispatch_nt<2>(nt, grid, out, q, k_cache, v_cache, block_tables, ctx_lens, nq, nkv, max_blocks,
-                                    block_size, bs_shift, sl2, part_o, part_ml, part_size, max_parts, rounds); break;
-        case 4: ok = dispatch_nt<4>(nt, grid, out, q, k_cache, v_cache, block_tables, ctx_lens, nq, nkv, max_blocks,
-                                    block_size, bs_shift, sl2, part_o, part_ml, part_size, max_parts, rounds); break;
-        case 8: ok = dispatch_nt<8>(nt, grid, out, q, k_cache, v_cache, block_tables, ctx_lens, nq, nkv, max_blocks,
-                                    block_size, bs_shift, sl2, part_o, part_ml, part_size, max_parts, rounds); break;
-        case 16: ok = dispatch_nt<16>(nt, grid, out, q, k_cache, v_cache, block_tables, ctx_lens, nq, nkv, max_blocks,
-                                      block_size, bs_shift, sl2, part_o, part_ml, part_size, max_parts, rounds); break;
-        default: break;
-    }
-    if (!ok) {
+    if (G != 1 && G != 2 && G != 4 && G != 8 && G != 16) {
         fprintf(stderr, "[llmgen-hip] attn_decode: unsupported GQA group size %d\n", G);
         return;
     }
-    hipLaunchKernelGGL(attn_decode_reduce_kernel, dim3(nq, S), dim3(HD), 0, g_llmgen_stream, out, part_o, part_ml,
-                       ctx_lens, nq, part_size, max_parts);
+    // Each workgroup takes k consecutive parts (span = k * part_size tokens, one partial result).  k grows
+    // with the launch so that a long-context launch has about 4 workgroups per compute unit, each streaming
+    // a long span with its loads pipelined, instead of many short workgroups; partial slots stay < max_parts.
+    const long total = (long)nkv * S * max_parts;
+    const long target = 4L * num_compute_units();
+    const int k = (int)(total > target ? total / target : 1);
+    const int nparts = (max_parts + k - 1) / k;
+    DecodeArgs a{out, q, k_cache, v_cache, block_tables, ctx_lens, nq, nkv, max_blocks, block_size,
+                 (block_size & (block_size - 1)) == 0 ? __builtin_ctz(block_size) : -1, scale * LLMGEN_LOG2E,
+                 part_o, part_ml, part_size * k, max_parts};
+    const dim3 grid(nkv, S, nparts);
+    switch (G) {
+        case 1: launch_pow2<1, 2>(grid, a); break;
+        case 2: launch_pow2<2, 2>(grid, a); break;
+        case 4: launch_pow2<4, 2>(grid, a); break;
+        case 8: launch_pow2<8, 2>(grid, a); break;
+        default: launch_pow2<16, 1>(grid, a); break;
+    }
+    hipLaunchKernelGGL(attn_decode_reduce_kernel, dim3(nkv, S), dim3(DEC_THREADS), 0, g_llmgen_stream, out, part_o,
+                       part_ml, ctx_lens, nq, G, a.span, nparts, max_parts);
 }

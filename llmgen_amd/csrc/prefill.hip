@@ -36,13 +36,6 @@ constexpr int VT_STRIDE = BK + 8;  // V^T tile row stride in bf16 (144 B)
 
 __device__ __forceinline__ int swap23(int b) { return (b & ~12) | ((b & 4) << 1) | ((b & 8) >> 1); }
 
-__device__ __forceinline__ long kv_row(const int *__restrict__ bt, int t, int block_size, int bs_shift, long head_off,
-                                       long blk_stride) {
-    const int bi = bs_shift >= 0 ? (t >> bs_shift) : (t / block_size);
-    const int off = t - bi * block_size;
-    return (long)bt[bi] * blk_stride + head_off + (long)off * HD;
-}
-
 // NW = waves per workgroup (2 per head: rows 0-31 and 32-63 of the tile).
 template <int NW>
 __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)))
@@ -110,19 +103,47 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
     u32x4_t vreg[V_ITEMS][2];
     auto prefetch = [&](int it) {
         const int kb0 = it * BK;
+        int kkey[K_ITEMS], vkey[V_ITEMS][2], kblk[K_ITEMS], vblk[V_ITEMS][2];
+#pragma unroll
+        for (int i = 0; i < K_ITEMS; ++i) kkey[i] = min(kb0 + ((tid + i * NT) >> 4), kend - 1);
+#pragma unroll
+        for (int i = 0; i < V_ITEMS; ++i) {
+            const int kp = (tid + i * NT) & 31;
+            vkey[i][0] = min(kb0 + 2 * kp, kend - 1);
+            vkey[i][1] = min(kb0 + 2 * kp + 1, kend - 1);
+        }
+        if (bs_shift >= 0 && block_size >= BK) {
+            // the tile's BK keys touch at most two blocks: two scalar block-table reads, then a per-lane select
+            const int b0 = kb0 >> bs_shift, b1 = min(kb0 + BK - 1, kend - 1) >> bs_shift;
+            const int p0 = bt[b0], p1 = bt[b1];
+#pragma unroll
+            for (int i = 0; i < K_ITEMS; ++i) kblk[i] = (kkey[i] >> bs_shift) == b0 ? p0 : p1;
+#pragma unroll
+            for (int i = 0; i < V_ITEMS; ++i)
+#pragma unroll
+                for (int e = 0; e < 2; ++e) vblk[i][e] = (vkey[i][e] >> bs_shift) == b0 ? p0 : p1;
+        } else {
+            // independent block-table reads first, then the K/V reads
+#pragma unroll
+            for (int i = 0; i < K_ITEMS; ++i) kblk[i] = bt[kkey[i] / block_size];
+#pragma unroll
+            for (int i = 0; i < V_ITEMS; ++i)
+#pragma unroll
+                for (int e = 0; e < 2; ++e) vblk[i][e] = bt[vkey[i][e] / block_size];
+        }
 #pragma unroll
         for (int i = 0; i < K_ITEMS; ++i) {
-            const int item = tid + i * NT;
-            const int key = min(kb0 + (item >> 4), kend - 1);
-            kreg[i] = ld16(kc + kv_row(bt, key, block_size, bs_shift, head_off, blk_stride) + (item & 15) * 8);
+            const int off = bs_shift >= 0 ? (kkey[i] & (block_size - 1)) : kkey[i] % block_size;
+            kreg[i] = ld16(kc + (long)kblk[i] * blk_stride + head_off + (long)off * HD + ((tid + i * NT) & 15) * 8);
         }
 #pragma unroll
         for (int i = 0; i < V_ITEMS; ++i) {
-            const int item = tid + i * NT;
-            const int kp = item & 31, dc = item >> 5;
-            const int k0 = min(kb0 + 2 * kp, kend - 1), k1 = min(kb0 + 2 * kp + 1, kend - 1);
-            vreg[i][0] = ld16(vc + kv_row(bt, k0, block_size, bs_shift, head_off, blk_stride) + dc * 8);
-            vreg[i][1] = ld16(vc + kv_row(bt, k1, block_size, bs_shift, head_off, blk_stride) + dc * 8);
+            const int dc = (tid + i * NT) >> 5;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const int off = bs_shift >= 0 ? (vkey[i][e] & (block_size - 1)) : vkey[i][e] % block_size;
+                vreg[i][e] = ld16(vc + (long)vblk[i][e] * blk_stride + head_off + (long)off * HD + dc * 8);
+            }
         }
     };
     auto commit = [&]() {
