@@ -93,3 +93,39 @@ def test_step_matches_oracle_sampled_rows(gpu, name):
     assert np.array_equal(to_u16(kc), okc), "store_kv K cache differs"
     assert np.array_equal(to_u16(vc), ovc), "store_kv V cache differs"
     compare(to_u16(out)[rows], of, name)
+
+
+def test_golden_vectors(gpu):
+    """The committed golden step (oracle outputs) through the C-ABI: store_kv + prefill launcher."""
+    import os
+
+    print("[gpu-test] golden", flush=True)
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "paged_attention_golden.npz"))
+    nq, nkv, hd, bs, mb = (int(x) for x in g["shape"])
+
+    def dev(a):
+        return torch.from_numpy(np.ascontiguousarray(a).view(np.int16) if a.dtype == np.uint16 else a).to("cuda")
+
+    kc, vc = dev(g["kc"]), dev(g["vc"])
+    q, k, v = dev(g["q"]), dev(g["k"]), dev(g["v"])
+    slots, bt, cu_q, ctx = dev(g["slots"]), dev(g["block_tables"]), dev(g["cu_q"]), dev(g["ctx"])
+    tile = lib().hip_attn_prefill_tile()
+    tseq, tq0 = [], []
+    cq = g["cu_q"]
+    for s in range(3):
+        for q0 in range(0, int(cq[s + 1] - cq[s]), tile):
+            tseq.append(s)
+            tq0.append(q0)
+    tseq = torch.tensor(tseq, dtype=torch.int32, device="cuda")
+    tq0 = torch.tensor(tq0, dtype=torch.int32, device="cuda")
+    out = torch.full((32, nq, hd), -1, dtype=torch.int16, device="cuda")
+    L = lib()
+    L.hip_store_kv(k.data_ptr(), v.data_ptr(), slots.data_ptr(), kc.data_ptr(), vc.data_ptr(), 32, nkv, hd, bs)
+    L.hip_attn_prefill(out.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(), bt.data_ptr(), ctx.data_ptr(),
+                       cu_q.data_ptr(), tseq.data_ptr(), tq0.data_ptr(), len(tseq), nq, nkv, hd, mb, bs,
+                       1 / math.sqrt(hd))
+    torch.cuda.synchronize()
+    check_hip_error("golden")
+    got = out.cpu().numpy().view(np.uint16)
+    compare(got, g["out_f32"], "golden")
+    assert not got[31].any(), "padding row not zero"
