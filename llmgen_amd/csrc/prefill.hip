@@ -26,6 +26,8 @@
 
 #include <math.h>
 
+#include <type_traits>
+
 namespace {
 
 constexpr int HD = 128;
@@ -38,7 +40,7 @@ __device__ __forceinline__ int swap23(int b) { return (b & ~12) | ((b & 4) << 1)
 
 // NW = waves per workgroup (2 per head: rows 0-31 and 32-63 of the tile).
 template <int NW>
-__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 2 ? 1 : 2)))
     attn_prefill_kernel(bf16_t *__restrict__ out, const bf16_t *__restrict__ q, const bf16_t *__restrict__ kc,
                         const bf16_t *__restrict__ vc, const int *__restrict__ block_tables,
                         const int *__restrict__ ctx_lens, const int *__restrict__ cu_q,
@@ -177,6 +179,75 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
         for (int r = 0; r < 16; ++r) o[db][r] = 0.f;
     float m_run = -INFINITY, l_run = 0.f;
 
+    // One 64-key tile for this wave: S^T = K Q^T, online softmax (base 2, scale folded into one FMA), O^T += V^T P^T.
+    auto tile_step = [&](int kb0, auto masked) {
+        constexpr bool MASK = decltype(masked)::value;
+        f32x16_t sacc[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
+        const bf16_t *kp = Ks + l32 * KS_STRIDE + hh * 8;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {  // two independent accumulation chains interleaved
+            const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t *>(kp + c * 16);
+            const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t *>(kp + 32 * KS_STRIDE + c * 16);
+            sacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qf[c], sacc[0], 0, 0, 0);
+            sacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qf[c], sacc[1], 0, 0, 0);
+        }
+        // lane holds row my_row, keys kb0 + kb*32 + (r/4)*8 + hh*4 + r%4 (raw dot products)
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                if (MASK) {
+                    const int key = kb0 + kb * 32 + (r >> 2) * 8 + hh * 4 + (r & 3);
+                    if (!row_valid || key > my_pos) sacc[kb][r] = -INFINITY;
+                }
+                mx = fmaxf(mx, sacc[kb][r]);
+            }
+        mx = fmaxf(mx, lane_xor(mx, 32)) * scale_log2;  // scale > 0 commutes with max
+        const float m_new = fmaxf(m_run, mx);
+        const float m_use = (MASK && m_new == -INFINITY) ? 0.f : m_new;
+        const float corr = fast_exp2(m_run - m_use);
+        const bool grew = m_new > m_run;
+        float lsum = 0.f;
+        bf16x8_t pf[4];  // B fragments for the four 16-key steps of P V
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                float p[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    p[e] = fast_exp2(__builtin_fmaf(sacc[kb][half * 8 + e], scale_log2, -m_use));
+                    lsum += p[e];
+                }
+                u32x4_t w;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) w[e] = pack_bf16x2(p[2 * e], p[2 * e + 1]);
+                pf[kb * 2 + half] = __builtin_bit_cast(bf16x8_t, w);
+            }
+        l_run = l_run * corr + lsum;
+        m_run = m_new;
+        if (__any(grew)) {  // rescale only when some row's running max moved (corr == 1 elsewhere)
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[db][r] *= corr;
+        }
+        // ---- O^T[dim][row] += V^T P^T: four independent accumulators per 16-key step ----
+        const bf16_t *vp = Vt + l32 * VT_STRIDE + hh * 8;
+#pragma unroll
+        for (int kc16 = 0; kc16 < 4; ++kc16)
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                const bf16x8_t a = *reinterpret_cast<const bf16x8_t *>(vp + db * 32 * VT_STRIDE + kc16 * 16);
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pf[kc16], o[db], 0, 0, 0);
+            }
+    };
+
     if (n_iter > 0) prefetch(0);
     for (int it = 0; it < n_iter; ++it) {
         const int kb0 = it * BK;
@@ -186,71 +257,11 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
         if (it + 1 < n_iter) prefetch(it + 1);
 
         if (wave_active && kb0 <= wave_pos_max) {
-            // ---- S^T[key][row] = K Q^T: two 32-key blocks x eight 16-dim steps ----
-            f32x16_t sacc[2];
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-                for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
-                const bf16_t *kp = Ks + (kb * 32 + l32) * KS_STRIDE + hh * 8;
-#pragma unroll
-                for (int c = 0; c < 8; ++c) {
-                    const bf16x8_t a = *reinterpret_cast<const bf16x8_t *>(kp + c * 16);
-                    sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[c], sacc[kb], 0, 0, 0);
-                }
-            }
-            // lane holds row my_row, keys kb0 + kb*32 + (r/4)*8 + hh*4 + r%4
-            const bool need_mask = wave_has_pad || (kb0 + BK - 1 > wave_pos_min);
-            float mx = -INFINITY;
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    float v = sacc[kb][r] * scale_log2;
-                    if (need_mask) {
-                        const int key = kb0 + kb * 32 + (r >> 2) * 8 + hh * 4 + (r & 3);
-                        if (!row_valid || key > my_pos) v = -INFINITY;
-                    }
-                    sacc[kb][r] = v;
-                    mx = fmaxf(mx, v);
-                }
-            mx = fmaxf(mx, lane_xor(mx, 32));
-            const float m_new = fmaxf(m_run, mx);
-            const float m_use = m_new == -INFINITY ? 0.f : m_new;
-            const float corr = fast_exp2(m_run - m_use);
-            float lsum = 0.f;
-            bf16x8_t pf[4];  // B fragments for the four 16-key steps of P V
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-                for (int half = 0; half < 2; ++half) {
-                    float p[8];
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        p[e] = fast_exp2(sacc[kb][half * 8 + e] - m_use);
-                        lsum += p[e];
-                    }
-                    u32x4_t w;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) w[e] = pack_bf16x2(p[2 * e], p[2 * e + 1]);
-                    pf[kb * 2 + half] = __builtin_bit_cast(bf16x8_t, w);
-                }
-            l_run = l_run * corr + lsum;
-            m_run = m_new;
-#pragma unroll
-            for (int db = 0; db < 4; ++db)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) o[db][r] *= corr;
-            // ---- O^T[dim][row] += V^T P^T ----
-#pragma unroll
-            for (int db = 0; db < 4; ++db) {
-                const bf16_t *vp = Vt + (db * 32 + l32) * VT_STRIDE + hh * 8;
-#pragma unroll
-                for (int kc16 = 0; kc16 < 4; ++kc16) {
-                    const bf16x8_t a = *reinterpret_cast<const bf16x8_t *>(vp + kc16 * 16);
-                    o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pf[kc16], o[db], 0, 0, 0);
-                }
-            }
+            // tiles wholly below the wave's diagonal (and with no padding rows) take the unmasked path
+            if (wave_has_pad || kb0 + BK - 1 > wave_pos_min)
+                tile_step(kb0, std::true_type{});
+            else
+                tile_step(kb0, std::false_type{});
         }
     }
 

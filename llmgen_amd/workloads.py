@@ -192,13 +192,35 @@ def make(name: str, seed: Optional[int] = None) -> Workload:
                         note="kernel_test decode: last row of ctx=150")
     if name == "cpu_mixed":
         # cpu/attention.zig:188-251 with head_dim 128 (the kernels' head size): nq=4, nkv=2, bs=16, 24 blocks,
-        # max_blocks=8; seq0 ctx=70 q_len=30, seq1 decode ctx=41, seq2 padding ctx=0
+        # max_blocks=8; seq0 ctx=70 q_len=30, seq1 decode ctx=41, seq2 padding ctx=0.  The reference test only
+        # attends, and its second table (i*7+2)%24 shares physical block 16 with the first; this step also writes
+        # this step's K/V, so seq1 uses (i*7+3)%24 and no two tokens write one slot.
         s = 11 if seed is None else seed
         t0 = [(i * 5 + 1) % 24 for i in range(8)]
-        t1 = [(i * 7 + 2) % 24 for i in range(8)]
+        t1 = [(i * 7 + 3) % 24 for i in range(8)]
         ents = [Entry(40, 30, t0), Entry(40, 1, t1)]
         return Workload(name, 4, 2, 128, 16, 24, 8, 128, ents, uniform=True, seed=s, decode=False, pad_rows=1,
                         note="cpu test: chunked tail + decode + padding row")
+    if name in ("gqa1", "gqa8", "gqa16"):
+        # small mixed steps at other group sizes: chunked tail + fresh prompt + decode rows, bs 32, permuted blocks
+        s = {"gqa1": 21, "gqa8": 22, "gqa16": 23}[name] if seed is None else seed
+        nq, nkv = {"gqa1": (8, 8), "gqa8": (16, 2), "gqa16": (32, 2)}[name]
+        rng = np.random.default_rng(s)
+        spec = [(200, 90), (0, 150), (333, 1), (64, 1), (0, 1)]
+        ctxs = [a + b for a, b in spec]
+        tables, nb = _tables(rng, ctxs, 32, permute=True, extra_blocks=3)
+        ents = [Entry(a, b, t) for (a, b), t in zip(spec, tables)]
+        return Workload(name, nq, nkv, 128, 32, nb, 12, 512, ents, std=1.0, seed=s, decode=False,
+                        note=f"mixed step at GQA {nq // nkv}")
+    if name in ("gqa1d", "gqa8d", "gqa16d"):
+        # decode-only steps at other group sizes (ragged contexts, one of them a single key), bs 32
+        s = {"gqa1d": 31, "gqa8d": 32, "gqa16d": 33}[name] if seed is None else seed
+        nq, nkv = {"gqa1d": (8, 8), "gqa8d": (16, 2), "gqa16d": (32, 2)}[name]
+        rng = np.random.default_rng(s)
+        ctxs = [290, 1500, 64, 700, 1]
+        tables, nb = _tables(rng, ctxs, 32, permute=True, extra_blocks=3)
+        return Workload(name, nq, nkv, 128, 32, nb, 48, 1536, _decode_entries(ctxs, tables), std=1.0, seed=s,
+                        note=f"decode step at GQA {nq // nkv}")
     raise KeyError(name)
 
 

@@ -54,6 +54,14 @@ def run_oracle(wl: Workload, t: dict, rows=None, threads: int = 1):
     return kc, vc, ob, of
 
 
+def assert_cache_equal(got: np.ndarray, ref: np.ndarray, what: str) -> None:
+    """Bit-exact paged-cache comparison; on mismatch name the (block, head, slot) rows that differ."""
+    if np.array_equal(got, ref):
+        return
+    bad = np.argwhere((got != ref).any(axis=-1))
+    raise AssertionError(f"{what}: {len(bad)} cache rows differ, first (block, head, slot): {bad[:8].tolist()}")
+
+
 def compare(got_bf16_u16: np.ndarray, ref_f32: np.ndarray, what: str, max_abs=MAX_ABS, rel_l2=REL_L2):
     g = oracle.bf16_to_f32(got_bf16_u16).astype(np.float64)
     r = ref_f32.astype(np.float64)

@@ -12,7 +12,7 @@ import pytest
 import torch
 
 import oracle
-from harness import check_hip_error, compare, run_gpu, run_oracle
+from harness import assert_cache_equal, check_hip_error, compare, run_gpu, run_oracle
 from llmgen_amd import attention as A
 from llmgen_amd._lib import lib
 from llmgen_amd.workloads import make, to_u16
@@ -34,15 +34,16 @@ def _sample_rows(wl, meta, n_random=48, seed=0):
     return np.array(sorted(rows), np.int32)
 
 
-@pytest.mark.parametrize("name", ["kt_prefill", "cpu_mixed", "c1", "c2"])
+@pytest.mark.parametrize("name", ["kt_prefill", "cpu_mixed", "c1", "c2", "gqa1", "gqa8", "gqa16",
+                                  "gqa1d", "gqa8d", "gqa16d"])
 def test_step_matches_oracle_all_rows(gpu, name):
     wl = make(name)
     print(f"[gpu-test] {name}", flush=True)
     t = wl.tensors(device="cuda")
     out, kc, vc = run_gpu(wl, t)
     okc, ovc, ob, of = run_oracle(wl, t)
-    assert np.array_equal(to_u16(kc), okc), "store_kv K cache differs"
-    assert np.array_equal(to_u16(vc), ovc), "store_kv V cache differs"
+    assert_cache_equal(to_u16(kc), okc, f"{name} store_kv K")
+    assert_cache_equal(to_u16(vc), ovc, f"{name} store_kv V")
     got = to_u16(out)
     compare(got, of, name)
     # padding rows (ctx < q_len) are exactly zero
@@ -81,7 +82,7 @@ def test_decode_part_size_sweep(gpu, part_size):
     compare(to_u16(out), of, f"kt_decode ps={part_size}")
 
 
-@pytest.mark.parametrize("name", ["c3", "c4"])
+@pytest.mark.parametrize("name", ["c3", "c4", "c5d", "c5p"])
 def test_step_matches_oracle_sampled_rows(gpu, name):
     wl = make(name)
     print(f"[gpu-test] {name}", flush=True)
@@ -90,8 +91,8 @@ def test_step_matches_oracle_sampled_rows(gpu, name):
     meta = wl.meta(lib().hip_attn_prefill_tile())
     rows = _sample_rows(wl, meta)
     okc, ovc, ob, of = run_oracle(wl, t, rows=rows, threads=16)
-    assert np.array_equal(to_u16(kc), okc), "store_kv K cache differs"
-    assert np.array_equal(to_u16(vc), ovc), "store_kv V cache differs"
+    assert_cache_equal(to_u16(kc), okc, f"{name} store_kv K")
+    assert_cache_equal(to_u16(vc), ovc, f"{name} store_kv V")
     compare(to_u16(out)[rows], of, name)
 
 

@@ -181,3 +181,13 @@ def test_operator_errors():
         A.PagedAttentionImpl.execute(0, A.AttnNode(out, [out, out, out], layer_id=3))
     A.g_attn_mgr = None
     assert A.FlashAttentionImpl is A.PagedAttentionImpl
+
+
+def test_workload_slots_are_unique():
+    """No two tokens of a step write the same KV slot (a racing pair would make store_kv order-dependent)."""
+    from llmgen_amd.workloads import make
+
+    for name in ("kt_prefill", "cpu_mixed", "c1", "c2", "c3", "c4", "gqa1", "gqa8", "gqa16", "gqa1d", "gqa8d"):
+        m = make(name).meta(64)
+        s = m.slots[m.slots >= 0]
+        assert len(np.unique(s)) == len(s), name
