@@ -35,11 +35,13 @@ constexpr int BQ = 64;            // query rows per tile (the value hip_attn_pre
 constexpr int BK = 64;            // keys per LDS tile
 constexpr int KS_STRIDE = HD + 8;  // K tile row stride in bf16 (272 B: rows shift by 4 banks)
 constexpr int VT_STRIDE = BK + 8;  // V^T tile row stride in bf16 (144 B)
+constexpr float RESCALE_LOG2 = 8.f;  // lazy-rescale threshold (log2 units)
 
 __device__ __forceinline__ int swap23(int b) { return (b & ~12) | ((b & 4) << 1) | ((b & 8) >> 1); }
 
-// NW = waves per workgroup (2 per head: rows 0-31 and 32-63 of the tile).
-template <int NW>
+// NW = waves per workgroup (2 per head: rows 0-31 and 32-63 of the tile); FAST = block_size is a power of two
+// and a multiple of BK (every K/V tile then lies inside one block).
+template <int NW, bool FAST>
 __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 2 ? 1 : 2)))
     attn_prefill_kernel(bf16_t *__restrict__ out, const bf16_t *__restrict__ q, const bf16_t *__restrict__ kc,
                         const bf16_t *__restrict__ vc, const int *__restrict__ block_tables,
@@ -105,6 +107,28 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
     u32x4_t vreg[V_ITEMS][2];
     auto prefetch = [&](int it) {
         const int kb0 = it * BK;
+        if (FAST) {
+            // block_size is a power of two and a multiple of BK, so the whole tile lies in one block: one
+            // scalar block-table read gives a scalar base, and every lane adds a 32-bit in-block offset
+            const int phys = bt[__builtin_amdgcn_readfirstlane(kb0 >> bs_shift)];
+            const long base = (long)phys * blk_stride + head_off + (long)(kb0 & (block_size - 1)) * HD;
+            const bf16_t *kt = kc + base;
+            const bf16_t *vt = vc + base;
+            const int last = kend - 1 - kb0;  // clamp: keys past kend reread the last valid key
+#pragma unroll
+            for (int i = 0; i < K_ITEMS; ++i) {
+                const int item = tid + i * NT;
+                kreg[i] = ld16(kt + min(item >> 4, last) * HD + (item & 15) * 8);
+            }
+#pragma unroll
+            for (int i = 0; i < V_ITEMS; ++i) {
+                const int item = tid + i * NT;
+                const int kp = item & 31, dc = item >> 5;
+                vreg[i][0] = ld16(vt + min(2 * kp, last) * HD + dc * 8);
+                vreg[i][1] = ld16(vt + min(2 * kp + 1, last) * HD + dc * 8);
+            }
+            return;
+        }
         int kkey[K_ITEMS], vkey[V_ITEMS][2], kblk[K_ITEMS], vblk[V_ITEMS][2];
 #pragma unroll
         for (int i = 0; i < K_ITEMS; ++i) kkey[i] = min(kb0 + ((tid + i * NT) >> 4), kend - 1);
@@ -114,28 +138,16 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
             vkey[i][0] = min(kb0 + 2 * kp, kend - 1);
             vkey[i][1] = min(kb0 + 2 * kp + 1, kend - 1);
         }
-        if (bs_shift >= 0 && block_size >= BK) {
-            // the tile's BK keys touch at most two blocks: two scalar block-table reads, then a per-lane select
-            const int b0 = kb0 >> bs_shift, b1 = min(kb0 + BK - 1, kend - 1) >> bs_shift;
-            const int p0 = bt[b0], p1 = bt[b1];
+        // generic block size: independent block-table reads first, then the K/V reads
 #pragma unroll
-            for (int i = 0; i < K_ITEMS; ++i) kblk[i] = (kkey[i] >> bs_shift) == b0 ? p0 : p1;
+        for (int i = 0; i < K_ITEMS; ++i) kblk[i] = bt[kkey[i] / block_size];
 #pragma unroll
-            for (int i = 0; i < V_ITEMS; ++i)
+        for (int i = 0; i < V_ITEMS; ++i)
 #pragma unroll
-                for (int e = 0; e < 2; ++e) vblk[i][e] = (vkey[i][e] >> bs_shift) == b0 ? p0 : p1;
-        } else {
-            // independent block-table reads first, then the K/V reads
-#pragma unroll
-            for (int i = 0; i < K_ITEMS; ++i) kblk[i] = bt[kkey[i] / block_size];
-#pragma unroll
-            for (int i = 0; i < V_ITEMS; ++i)
-#pragma unroll
-                for (int e = 0; e < 2; ++e) vblk[i][e] = bt[vkey[i][e] / block_size];
-        }
+            for (int e = 0; e < 2; ++e) vblk[i][e] = bt[vkey[i][e] / block_size];
 #pragma unroll
         for (int i = 0; i < K_ITEMS; ++i) {
-            const int off = bs_shift >= 0 ? (kkey[i] & (block_size - 1)) : kkey[i] % block_size;
+            const int off = kkey[i] % block_size;
             kreg[i] = ld16(kc + (long)kblk[i] * blk_stride + head_off + (long)off * HD + ((tid + i * NT) & 15) * 8);
         }
 #pragma unroll
@@ -143,7 +155,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
             const int dc = (tid + i * NT) >> 5;
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
-                const int off = bs_shift >= 0 ? (vkey[i][e] & (block_size - 1)) : vkey[i][e] % block_size;
+                const int off = vkey[i][e] % block_size;
                 vreg[i][e] = ld16(vc + (long)vblk[i][e] * blk_stride + head_off + (long)off * HD + dc * 8);
             }
         }
@@ -208,10 +220,12 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
                 mx = fmaxf(mx, sacc[kb][r]);
             }
         mx = fmaxf(mx, lane_xor(mx, 32)) * scale_log2;  // scale > 0 commutes with max
-        const float m_new = fmaxf(m_run, mx);
+        // Lazy rescaling: the reference max m_run only moves when a row's max exceeds it by more than
+        // RESCALE_LOG2 (or on the first keys), so the o rescale below is rare; probabilities stay <= 2^8.
+        const bool grow = mx > m_run + RESCALE_LOG2;
+        const float m_new = grow ? mx : m_run;
         const float m_use = (MASK && m_new == -INFINITY) ? 0.f : m_new;
-        const float corr = fast_exp2(m_run - m_use);
-        const bool grew = m_new > m_run;
+        const float corr = grow ? fast_exp2(m_run - m_use) : 1.f;
         float lsum = 0.f;
         bf16x8_t pf[4];  // B fragments for the four 16-key steps of P V
 #pragma unroll
@@ -231,7 +245,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
             }
         l_run = l_run * corr + lsum;
         m_run = m_new;
-        if (__any(grew)) {  // rescale only when some row's running max moved (corr == 1 elsewhere)
+        if (__any(grow)) {  // corr == 1 in rows that did not move
 #pragma unroll
             for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -283,13 +297,18 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
 }
 
 template <int NW>
-void launch_prefill(int head_groups, bf16_t *out, const bf16_t *q, const bf16_t *kc, const bf16_t *vc, const int *bt,
+void launch_prefill(bool fast, int head_groups, bf16_t *out, const bf16_t *q, const bf16_t *kc, const bf16_t *vc, const int *bt,
                     const int *ctx, const int *cu_q, const int *tile_seq, const int *tile_q0, int n_tiles, int nq,
                     int nkv, int G, int max_blocks, int block_size, int bs_shift, float sl2) {
     const long grid = (long)n_tiles * nkv * head_groups;
-    hipLaunchKernelGGL((attn_prefill_kernel<NW>), dim3((unsigned)grid), dim3(64 * NW), 0, g_llmgen_stream, out, q, kc,
-                       vc, bt, ctx, cu_q, tile_seq, tile_q0, n_tiles, nq, nkv, G, head_groups, max_blocks,
-                       block_size, bs_shift, sl2);
+    if (fast)
+        hipLaunchKernelGGL((attn_prefill_kernel<NW, true>), dim3((unsigned)grid), dim3(64 * NW), 0, g_llmgen_stream,
+                           out, q, kc, vc, bt, ctx, cu_q, tile_seq, tile_q0, n_tiles, nq, nkv, G, head_groups,
+                           max_blocks, block_size, bs_shift, sl2);
+    else
+        hipLaunchKernelGGL((attn_prefill_kernel<NW, false>), dim3((unsigned)grid), dim3(64 * NW), 0, g_llmgen_stream,
+                           out, q, kc, vc, bt, ctx, cu_q, tile_seq, tile_q0, n_tiles, nq, nkv, G, head_groups,
+                           max_blocks, block_size, bs_shift, sl2);
 }
 
 }  // namespace
@@ -315,16 +334,17 @@ extern "C" void hip_attn_prefill(bf16_t *out, const bf16_t *q, const bf16_t *k_c
         return;
     }
     const int bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz(block_size) : -1;
+    const bool fast = bs_shift >= 0 && block_size % BK == 0;
     const float sl2 = scale * LLMGEN_LOG2E;
     // two waves per head; at most 8 waves (4 heads) per workgroup, the rest of the group in further workgroups
     const int heads_per_wg = G < 4 ? G : 4;
     const int head_groups = G / heads_per_wg;
     switch (heads_per_wg) {
-        case 1: launch_prefill<2>(head_groups, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq,
+        case 1: launch_prefill<2>(fast, head_groups, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq,
                                   tile_q0, n_tiles, nq, nkv, G, max_blocks, block_size, bs_shift, sl2); break;
-        case 2: launch_prefill<4>(head_groups, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq,
+        case 2: launch_prefill<4>(fast, head_groups, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq,
                                   tile_q0, n_tiles, nq, nkv, G, max_blocks, block_size, bs_shift, sl2); break;
-        default: launch_prefill<8>(head_groups, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq,
+        default: launch_prefill<8>(fast, head_groups, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq,
                                    tile_q0, n_tiles, nq, nkv, G, max_blocks, block_size, bs_shift, sl2); break;
     }
 }
