@@ -23,6 +23,7 @@
 #include "hip_common.h"
 
 #include <math.h>
+#include <stdlib.h>
 
 namespace {
 
@@ -40,8 +41,8 @@ __device__ __forceinline__ int blk_index(int t, int block_size, int bs_shift) {
 // tokens).  Each workgroup streams `span` tokens of one (kv head, sequence) pair: round r+1's block-table and
 // K/V loads are issued before round r is computed (register double buffering), so every wave keeps one round
 // of loads in flight while it computes.
-template <int G, int NT, bool POW2>
-__global__ void __launch_bounds__(DEC_THREADS)
+template <int G, int NT, bool POW2, bool PIPE>
+__global__ void __launch_bounds__(DEC_THREADS) __attribute__((amdgpu_waves_per_eu(G >= 16 ? 1 : (PIPE || G >= 8 ? 2 : (G >= 4 ? 3 : 4)))))
     attn_decode_split_kernel(bf16_t *__restrict__ out, float *__restrict__ part_o, float *__restrict__ part_ml,
                              const bf16_t *__restrict__ q, const bf16_t *__restrict__ kc,
                              const bf16_t *__restrict__ vc, const int *__restrict__ block_tables,
@@ -213,14 +214,22 @@ __global__ void __launch_bounds__(DEC_THREADS)
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     };
 
-    Buf bufA, bufB;
-    load(0, bufA);
-    for (int r = 0; r < rounds; r += 2) {
-        if (r + 1 < rounds) load(r + 1, bufB);
-        compute(r, bufA);
-        if (r + 1 >= rounds) break;
-        if (r + 2 < rounds) load(r + 2, bufA);
-        compute(r + 1, bufB);
+    if (PIPE) {
+        Buf bufA, bufB;
+        load(0, bufA);
+        for (int r = 0; r < rounds; r += 2) {
+            if (r + 1 < rounds) load(r + 1, bufB);
+            compute(r, bufA);
+            if (r + 1 >= rounds) break;
+            if (r + 2 < rounds) load(r + 2, bufA);
+            compute(r + 1, bufB);
+        }
+    } else {  // one buffer, twice the occupancy: short spans rely on other waves to hide latency
+        Buf buf;
+        for (int r = 0; r < rounds; ++r) {
+            load(r, buf);
+            compute(r, buf);
+        }
     }
 
     // ---- per-wave totals ----
@@ -325,19 +334,31 @@ struct DecodeArgs {
     int span, max_parts;
 };
 
-template <int G, int NT, bool POW2>
+template <int G, int NT, bool POW2, bool PIPE>
 void launch_split(dim3 grid, const DecodeArgs &a) {
-    hipLaunchKernelGGL((attn_decode_split_kernel<G, NT, POW2>), grid, dim3(DEC_THREADS), 0, g_llmgen_stream, a.out,
+    hipLaunchKernelGGL((attn_decode_split_kernel<G, NT, POW2, PIPE>), grid, dim3(DEC_THREADS), 0, g_llmgen_stream, a.out,
                        a.part_o, a.part_ml, a.q, a.kc, a.vc, a.bt, a.ctx, a.nq, a.nkv, a.max_blocks, a.block_size,
                        a.bs_shift, a.sl2, a.span, a.max_parts);
 }
 
 template <int G, int NT>
-void launch_pow2(dim3 grid, const DecodeArgs &a) {
-    if (a.bs_shift >= 0)
-        launch_split<G, NT, true>(grid, a);
-    else
-        launch_split<G, NT, false>(grid, a);
+void launch_pow2(dim3 grid, const DecodeArgs &a, bool pipe) {
+    if (a.bs_shift >= 0) {
+        if (pipe)
+            launch_split<G, NT, true, true>(grid, a);
+        else
+            launch_split<G, NT, true, false>(grid, a);
+    } else {
+        if (pipe)
+            launch_split<G, NT, false, true>(grid, a);
+        else
+            launch_split<G, NT, false, false>(grid, a);
+    }
+}
+
+int env_int(const char *name, int dflt) {
+    const char *v = getenv(name);
+    return v && *v ? atoi(v) : dflt;
 }
 
 int num_compute_units() {
@@ -373,22 +394,27 @@ extern "C" void hip_attn_decode(bf16_t *out, const bf16_t *q, const bf16_t *k_ca
         return;
     }
     // Each workgroup takes k consecutive parts (span = k * part_size tokens, one partial result).  k grows
-    // with the launch so that a long-context launch has about 4 workgroups per compute unit, each streaming
+    // with the launch so that a long-context launch has about 2 workgroups per compute unit, each streaming
     // a long span with its loads pipelined, instead of many short workgroups; partial slots stay < max_parts.
     const long total = (long)nkv * S * max_parts;
-    const long target = 4L * num_compute_units();
+    static const int wg_per_cu = env_int("LLMGEN_DECODE_WG_PER_CU", 2);
+    const long target = (long)wg_per_cu * num_compute_units();
     const int k = (int)(total > target ? total / target : 1);
     const int nparts = (max_parts + k - 1) / k;
     DecodeArgs a{out, q, k_cache, v_cache, block_tables, ctx_lens, nq, nkv, max_blocks, block_size,
                  (block_size & (block_size - 1)) == 0 ? __builtin_ctz(block_size) : -1, scale * LLMGEN_LOG2E,
                  part_o, part_ml, part_size * k, max_parts};
     const dim3 grid(nkv, S, nparts);
+    // single-buffered rounds at 3-4 waves per SIMD measure faster than register double buffering at 2 (c2,
+    // c5d); GQA groups of 8+ need the registers for o anyway
+    static const int pipe_env = env_int("LLMGEN_DECODE_PIPE", -1);
+    const bool pipe = pipe_env >= 0 ? pipe_env != 0 : G >= 8;
     switch (G) {
-        case 1: launch_pow2<1, 2>(grid, a); break;
-        case 2: launch_pow2<2, 2>(grid, a); break;
-        case 4: launch_pow2<4, 2>(grid, a); break;
-        case 8: launch_pow2<8, 2>(grid, a); break;
-        default: launch_pow2<16, 1>(grid, a); break;
+        case 1: launch_pow2<1, 2>(grid, a, pipe); break;
+        case 2: launch_pow2<2, 2>(grid, a, pipe); break;
+        case 4: launch_pow2<4, 2>(grid, a, pipe); break;
+        case 8: launch_pow2<8, 2>(grid, a, pipe); break;
+        default: launch_pow2<16, 1>(grid, a, pipe); break;
     }
     hipLaunchKernelGGL(attn_decode_reduce_kernel, dim3(nkv, S), dim3(DEC_THREADS), 0, g_llmgen_stream, out, part_o,
                        part_ml, ctx_lens, nq, G, a.span, nparts, max_parts);
