@@ -47,15 +47,22 @@ __global__ void __launch_bounds__(DEC_THREADS) __attribute__((amdgpu_waves_per_e
                              const bf16_t *__restrict__ q, const bf16_t *__restrict__ kc,
                              const bf16_t *__restrict__ vc, const int *__restrict__ block_tables,
                              const int *__restrict__ ctx_lens, int nq, int nkv, int max_blocks, int block_size,
-                             int bs_shift, float scale_log2, int span, int max_parts) {
+                             int bs_shift, float scale_log2, int span, int max_parts, int nparts,
+                             int *__restrict__ counters) {
     constexpr int WTOK = NT * 16;              // tokens per wave per round
     constexpr int RTOK = DEC_WAVES * WTOK;     // tokens per round
     const int kvh = blockIdx.x, s = blockIdx.y, part = blockIdx.z;
     const int ctx = ctx_lens[s];
     const int t0 = part * span;
-    if (t0 >= ctx) return;
+    if (t0 >= ctx) {
+        if (ctx <= 0 && part == 0 && counters) {  // padding row: zeros (cpu/attention.zig:80-83)
+            for (int idx = threadIdx.x; idx < G * HD; idx += DEC_THREADS)
+                out[((long)s * nq + (long)kvh * G + idx / HD) * HD + idx % HD] = 0;
+        }
+        return;
+    }
     const int n = min(ctx - t0, span);
-    const int np = (ctx + span - 1) / span;
+    const int np = min((ctx + span - 1) / span, nparts);
     const int rounds = (n + RTOK - 1) / RTOK;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 15, rgrp = lane >> 4;
@@ -280,13 +287,54 @@ __global__ void __launch_bounds__(DEC_THREADS) __attribute__((amdgpu_waves_per_e
             out[((long)s * nq + h) * HD + d] = __builtin_bit_cast(bf16_t, (__bf16)(acc / L));
         } else {
             const long slot = ((long)s * nq + h) * max_parts + part;
-            part_o[slot * HD + d] = acc;
-            if (d == 0) {
-                part_ml[slot * 2] = M;
-                part_ml[slot * 2 + 1] = L;
+            if (counters) {  // device-coherent (write-through) stores: read by another workgroup below
+                __hip_atomic_store(part_o + slot * HD + d, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (d == 0) {
+                    __hip_atomic_store(part_ml + slot * 2, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(part_ml + slot * 2 + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            } else {
+                part_o[slot * HD + d] = acc;
+                if (d == 0) {
+                    part_ml[slot * 2] = M;
+                    part_ml[slot * 2 + 1] = L;
+                }
             }
         }
     }
+    if (np == 1 || !counters) return;
+
+    // ---- cross-workgroup merge: the last workgroup of this (kv head, sequence) to finish combines the np
+    //      partial results (attention.cu:186-207 semantics, m in base 2).  The partials were written with
+    //      device-coherent stores; each thread waits for its stores to complete before the barrier, then one
+    //      counter increment per workgroup elects the merger, which reads the partials with device-coherent
+    //      loads.  No cache-wide fence (an L2 write-back + invalidate per workgroup costs more than the whole
+    //      merge).  The merger resets the counter, so it is zero again when the kernel ends. ----
+    __shared__ int s_last;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    int *cnt = counters + (long)s * nkv + kvh;
+    if (tid == 0) s_last = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == np - 1;
+    __syncthreads();
+    if (!s_last) return;
+    for (int idx = tid; idx < G * HD; idx += DEC_THREADS) {
+        const int g = idx / HD, d = idx % HD;
+        const long h = (long)kvh * G + g;
+        float *ml = part_ml + ((long)s * nq + h) * max_parts * 2;
+        float *po = part_o + ((long)s * nq + h) * max_parts * HD + d;
+        float M = -INFINITY;
+        for (int p = 0; p < np; ++p)
+            M = fmaxf(M, __hip_atomic_load(ml + 2 * p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        float num = 0.f, den = 0.f;
+        for (int p = 0; p < np; ++p) {
+            const float w =
+                fast_exp2(__hip_atomic_load(ml + 2 * p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - M);
+            num += w * __hip_atomic_load(po + (long)p * HD, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            den += w * __hip_atomic_load(ml + 2 * p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        out[((long)s * nq + h) * HD + d] = __builtin_bit_cast(bf16_t, (__bf16)(num / den));
+    }
+    if (tid == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // attention.cu:186-207 semantics: out = sum_p 2^(m_p - M) o_p / sum_p 2^(m_p - M) l_p (m in base 2 here).
@@ -331,14 +379,15 @@ struct DecodeArgs {
     int nq, nkv, max_blocks, block_size, bs_shift;
     float sl2;
     float *part_o, *part_ml;
-    int span, max_parts;
+    int span, max_parts, nparts;
+    int *counters;  // merge counters (nullptr: the separate merge kernel runs)
 };
 
 template <int G, int NT, bool POW2, bool PIPE>
 void launch_split(dim3 grid, const DecodeArgs &a) {
     hipLaunchKernelGGL((attn_decode_split_kernel<G, NT, POW2, PIPE>), grid, dim3(DEC_THREADS), 0, g_llmgen_stream, a.out,
                        a.part_o, a.part_ml, a.q, a.kc, a.vc, a.bt, a.ctx, a.nq, a.nkv, a.max_blocks, a.block_size,
-                       a.bs_shift, a.sl2, a.span, a.max_parts);
+                       a.bs_shift, a.sl2, a.span, a.max_parts, a.nparts, a.counters);
 }
 
 template <int G, int NT>
@@ -359,6 +408,24 @@ void launch_pow2(dim3 grid, const DecodeArgs &a, bool pipe) {
 int env_int(const char *name, int dflt) {
     const char *v = getenv(name);
     return v && *v ? atoi(v) : dflt;
+}
+
+// Merge counters for the in-kernel split-K merge, one per (sequence, kv head).  They start at zero when the
+// library loads and every merging workgroup resets its own, so they are zero between launches.  Launches that
+// overlap on two streams must not share the library (as they must not share part_o / part_ml).
+constexpr int MAX_MERGE_SEGMENTS = 1 << 18;
+__device__ int g_merge_counters[MAX_MERGE_SEGMENTS];
+
+int *merge_counters() {
+    static int *ptr[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    if (!ptr[dev]) {
+        void *p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_merge_counters)) != hipSuccess) return nullptr;
+        ptr[dev] = (int *)p;
+    }
+    return ptr[dev];
 }
 
 int num_compute_units() {
@@ -401,9 +468,10 @@ extern "C" void hip_attn_decode(bf16_t *out, const bf16_t *q, const bf16_t *k_ca
     const long target = (long)wg_per_cu * num_compute_units();
     const int k = (int)(total > target ? total / target : 1);
     const int nparts = (max_parts + k - 1) / k;
+    int *counters = (long)S * nkv <= MAX_MERGE_SEGMENTS ? merge_counters() : nullptr;
     DecodeArgs a{out, q, k_cache, v_cache, block_tables, ctx_lens, nq, nkv, max_blocks, block_size,
                  (block_size & (block_size - 1)) == 0 ? __builtin_ctz(block_size) : -1, scale * LLMGEN_LOG2E,
-                 part_o, part_ml, part_size * k, max_parts};
+                 part_o, part_ml, part_size * k, max_parts, nparts, counters};
     const dim3 grid(nkv, S, nparts);
     // single-buffered rounds at 3-4 waves per SIMD measure faster than register double buffering at 2 (c2,
     // c5d); GQA groups of 8+ need the registers for o anyway
@@ -416,6 +484,7 @@ extern "C" void hip_attn_decode(bf16_t *out, const bf16_t *q, const bf16_t *k_ca
         case 8: launch_pow2<8, 2>(grid, a, pipe); break;
         default: launch_pow2<16, 1>(grid, a, pipe); break;
     }
-    hipLaunchKernelGGL(attn_decode_reduce_kernel, dim3(nkv, S), dim3(DEC_THREADS), 0, g_llmgen_stream, out, part_o,
-                       part_ml, ctx_lens, nq, G, a.span, nparts, max_parts);
+    if (!counters)  // batches beyond the counter array merge in a second kernel
+        hipLaunchKernelGGL(attn_decode_reduce_kernel, dim3(nkv, S), dim3(DEC_THREADS), 0, g_llmgen_stream, out,
+                           part_o, part_ml, ctx_lens, nq, G, a.span, nparts, max_parts);
 }
