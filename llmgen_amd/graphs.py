@@ -5,8 +5,9 @@ step metadata with padding rows only (ctx = 0, slot = -1), runs the nodes once e
 captures them on the global stream.  ``executor.zig:541-575`` picks the smallest bucket >= S, rewrites the
 metadata in place (same layout, so the recorded pointers stay valid) with one host-to-device copy, and replays.
 
-Here the recorded nodes are one layer's attention step, store_kv + split-K decode, with buffers owned by the
-bucket (q / k / v / out of ``bucket`` rows, the packed metadata and the split-K scratch) -- exactly the fixed
+Here the recorded nodes are the attention steps (store_kv + split-K decode) of one or more layers -- the engine
+records all decoder layers of a step in one graph, each layer with its own KV pools -- with buffers owned by
+the bucket (q / k / v / out of ``bucket`` rows, the packed metadata and the split-K scratch), exactly the fixed
 pointers the engine's activation pool gives the captured kernels.
 """
 from __future__ import annotations
@@ -38,10 +39,12 @@ class Bucket:
 class DecodeGraphs:
     """Captured store_kv + decode steps, one per bucket size, over one layer's KV pools."""
 
-    def __init__(self, layer: A.LayerState, nq: int, nkv: int, hd: int, block_size: int, max_blocks: int,
+    def __init__(self, layer, nq: int, nkv: int, hd: int, block_size: int, max_blocks: int,
                  max_model_len: int, max_seqs: int, buckets: Sequence[int] = None):
+        """``layer``: one LayerState, or a list of them (one per decoder layer, recorded in order)."""
         A.init_device()
-        self.layer, self.nq, self.nkv, self.hd = layer, nq, nkv, hd
+        self.layers = list(layer) if isinstance(layer, (list, tuple)) else [layer]
+        self.layer, self.nq, self.nkv, self.hd = self.layers[0], nq, nkv, hd
         self.block_size, self.max_blocks, self.max_model_len = block_size, max_blocks, max_model_len
         sizes = list(buckets) if buckets is not None else stepmod.decode_buckets(max_seqs)
         self.buckets: Dict[int, Bucket] = {}
@@ -49,14 +52,13 @@ class DecodeGraphs:
             self.buckets[bs] = self._capture(bs)
         self.sizes: List[int] = sorted(self.buckets)
 
-    def _node(self, b: Bucket) -> A.AttnNode:
-        return A.AttnNode(b.out, [b.q, b.k, b.v], layer_id=0)
-
     def _run_nodes(self, b: Bucket) -> None:
         mgr = A.PagedAttentionManager()
-        mgr.layers[0] = self.layer
+        for i, st in enumerate(self.layers):
+            mgr.layers[i] = st
         A.g_attn_mgr = mgr
-        A.PagedAttentionImpl.execute(0, self._node(b))
+        for i in range(len(self.layers)):
+            A.PagedAttentionImpl.execute(0, A.AttnNode(b.out, [b.q, b.k, b.v], layer_id=i))
 
     def _capture(self, size: int) -> Bucket:
         dev = self.layer.k.device
