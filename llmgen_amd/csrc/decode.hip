@@ -48,16 +48,25 @@ __global__ void __launch_bounds__(DEC_THREADS) __attribute__((amdgpu_waves_per_e
                              const bf16_t *__restrict__ vc, const int *__restrict__ block_tables,
                              const int *__restrict__ ctx_lens, int nq, int nkv, int max_blocks, int block_size,
                              int bs_shift, float scale_log2, int span, int max_parts, int nparts,
-                             int *__restrict__ counters) {
+                             int *__restrict__ counters, const int *__restrict__ cu_q,
+                             const int *__restrict__ tile_seq) {
     constexpr int WTOK = NT * 16;              // tokens per wave per round
     constexpr int RTOK = DEC_WAVES * WTOK;     // tokens per round
-    const int kvh = blockIdx.x, s = blockIdx.y, part = blockIdx.z;
+    const int kvh = blockIdx.x, part = blockIdx.z;
+    // decode launch: blockIdx.y is the sequence and its query row.  Prefill-metadata launch (cu_q != null):
+    // blockIdx.y is a query tile; only single-row segments (decode rows of a mixed step) are handled here.
+    int s = blockIdx.y, row = blockIdx.y;
+    if (cu_q) {
+        s = tile_seq[blockIdx.y];
+        row = cu_q[s];
+        if (cu_q[s + 1] - row != 1) return;
+    }
     const int ctx = ctx_lens[s];
     const int t0 = part * span;
     if (t0 >= ctx) {
-        if (ctx <= 0 && part == 0 && counters) {  // padding row: zeros (cpu/attention.zig:80-83)
+        if (ctx <= 0 && part == 0) {  // padding row: zeros (cpu/attention.zig:80-83)
             for (int idx = threadIdx.x; idx < G * HD; idx += DEC_THREADS)
-                out[((long)s * nq + (long)kvh * G + idx / HD) * HD + idx % HD] = 0;
+                out[((long)row * nq + (long)kvh * G + idx / HD) * HD + idx % HD] = 0;
         }
         return;
     }
@@ -81,7 +90,7 @@ __global__ void __launch_bounds__(DEC_THREADS) __attribute__((amdgpu_waves_per_e
     // A operand: row g = col holds head kvh*G+g; lane group rgrp holds dims c*32 + rgrp*8 .. +8 of chunk c.
     bf16x8_t qa[4];
     {
-        const bf16_t *qrow = q + ((long)s * nq + (long)kvh * G + (col < G ? col : 0)) * HD + rgrp * 8;
+        const bf16_t *qrow = q + ((long)row * nq + (long)kvh * G + (col < G ? col : 0)) * HD + rgrp * 8;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             u32x4_t v = ld16(qrow + c * 32);
@@ -284,7 +293,7 @@ __global__ void __launch_bounds__(DEC_THREADS) __attribute__((amdgpu_waves_per_e
         }
         const long h = (long)kvh * G + g;
         if (np == 1) {
-            out[((long)s * nq + h) * HD + d] = __builtin_bit_cast(bf16_t, (__bf16)(acc / L));
+            out[((long)row * nq + h) * HD + d] = __builtin_bit_cast(bf16_t, (__bf16)(acc / L));
         } else {
             const long slot = ((long)s * nq + h) * max_parts + part;
             if (counters) {  // device-coherent (write-through) stores: read by another workgroup below
@@ -381,13 +390,16 @@ struct DecodeArgs {
     float *part_o, *part_ml;
     int span, max_parts, nparts;
     int *counters;  // merge counters (nullptr: the separate merge kernel runs)
+    const int *cu_q = nullptr, *tile_seq = nullptr;  // prefill-metadata launch (single-row segments)
+    hipStream_t stream = nullptr;                    // nullptr: the library's launch stream
 };
 
 template <int G, int NT, bool POW2, bool PIPE>
 void launch_split(dim3 grid, const DecodeArgs &a) {
-    hipLaunchKernelGGL((attn_decode_split_kernel<G, NT, POW2, PIPE>), grid, dim3(DEC_THREADS), 0, g_llmgen_stream, a.out,
+    hipLaunchKernelGGL((attn_decode_split_kernel<G, NT, POW2, PIPE>), grid, dim3(DEC_THREADS), 0,
+                       a.stream ? a.stream : g_llmgen_stream, a.out,
                        a.part_o, a.part_ml, a.q, a.kc, a.vc, a.bt, a.ctx, a.nq, a.nkv, a.max_blocks, a.block_size,
-                       a.bs_shift, a.sl2, a.span, a.max_parts, a.nparts, a.counters);
+                       a.bs_shift, a.sl2, a.span, a.max_parts, a.nparts, a.counters, a.cu_q, a.tile_seq);
 }
 
 template <int G, int NT>
@@ -439,6 +451,20 @@ int num_compute_units() {
     return n;
 }
 
+void launch_decode_rows(dim3 grid, const DecodeArgs &a, int G) {
+    // single-buffered rounds at 3-4 waves per SIMD measure faster than register double buffering at 2 (c2,
+    // c5d); GQA groups of 8+ need the registers for o anyway
+    static const int pipe_env = env_int("LLMGEN_DECODE_PIPE", -1);
+    const bool pipe = pipe_env >= 0 ? pipe_env != 0 : G >= 8;
+    switch (G) {
+        case 1: launch_pow2<1, 2>(grid, a, pipe); break;
+        case 2: launch_pow2<2, 2>(grid, a, pipe); break;
+        case 4: launch_pow2<4, 2>(grid, a, pipe); break;
+        case 8: launch_pow2<8, 2>(grid, a, pipe); break;
+        default: launch_pow2<16, 1>(grid, a, pipe); break;
+    }
+}
+
 }  // namespace
 
 extern "C" void hip_attn_decode(bf16_t *out, const bf16_t *q, const bf16_t *k_cache, const bf16_t *v_cache,
@@ -472,19 +498,23 @@ extern "C" void hip_attn_decode(bf16_t *out, const bf16_t *q, const bf16_t *k_ca
     DecodeArgs a{out, q, k_cache, v_cache, block_tables, ctx_lens, nq, nkv, max_blocks, block_size,
                  (block_size & (block_size - 1)) == 0 ? __builtin_ctz(block_size) : -1, scale * LLMGEN_LOG2E,
                  part_o, part_ml, part_size * k, max_parts, nparts, counters};
-    const dim3 grid(nkv, S, nparts);
-    // single-buffered rounds at 3-4 waves per SIMD measure faster than register double buffering at 2 (c2,
-    // c5d); GQA groups of 8+ need the registers for o anyway
-    static const int pipe_env = env_int("LLMGEN_DECODE_PIPE", -1);
-    const bool pipe = pipe_env >= 0 ? pipe_env != 0 : G >= 8;
-    switch (G) {
-        case 1: launch_pow2<1, 2>(grid, a, pipe); break;
-        case 2: launch_pow2<2, 2>(grid, a, pipe); break;
-        case 4: launch_pow2<4, 2>(grid, a, pipe); break;
-        case 8: launch_pow2<8, 2>(grid, a, pipe); break;
-        default: launch_pow2<16, 1>(grid, a, pipe); break;
-    }
+    launch_decode_rows(dim3(nkv, S, nparts), a, G);
     if (!counters)  // batches beyond the counter array merge in a second kernel
         hipLaunchKernelGGL(attn_decode_reduce_kernel, dim3(nkv, S), dim3(DEC_THREADS), 0, g_llmgen_stream, out,
                            part_o, part_ml, ctx_lens, nq, G, a.span, nparts, max_parts);
 }
+
+// Decode rows of a prefill / mixed step (segments with q_len == 1): one workgroup per (kv head, tile) streams the
+// whole context and writes the row directly; no split-K scratch is needed.  The MFMA prefill kernel skips these
+// tiles.  Called by hip_attn_prefill.
+void llmgen_decode_rows_of_prefill(bf16_t *out, const bf16_t *q, const bf16_t *k_cache, const bf16_t *v_cache,
+                                   const int *block_tables, const int *ctx_lens, const int *cu_q,
+                                   const int *tile_seq, int n_tiles, int nq, int nkv, int max_blocks,
+                                   int block_size, float scale, hipStream_t stream) {
+    const int G = nq / nkv;
+    DecodeArgs a{out, q, k_cache, v_cache, block_tables, ctx_lens, nq, nkv, max_blocks, block_size,
+                 (block_size & (block_size - 1)) == 0 ? __builtin_ctz(block_size) : -1, scale * LLMGEN_LOG2E,
+                 nullptr, nullptr, 1 << 30, 1, 1, nullptr, cu_q, tile_seq, stream};
+    launch_decode_rows(dim3(nkv, n_tiles, 1), a, G);
+}
+

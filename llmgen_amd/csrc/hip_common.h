@@ -77,3 +77,16 @@ __device__ __forceinline__ float lane_xor(float x, int mask) {
 __device__ __forceinline__ u32x4_t ld16(const void *p) { return *reinterpret_cast<const u32x4_t *>(p); }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Internal (not exported): decode rows (segments with q_len == 1) of a prefill / mixed step, streamed by the
+// split-K decode kernel; defined in decode.hip, launched by hip_attn_prefill.
+__attribute__((visibility("hidden"))) void llmgen_decode_rows_of_prefill(
+    bf16_t *out, const bf16_t *q, const bf16_t *k_cache, const bf16_t *v_cache,
+                                   const int *block_tables, const int *ctx_lens, const int *cu_q,
+                                   const int *tile_seq, int n_tiles, int nq, int nkv, int max_blocks,
+                                   int block_size, float scale, hipStream_t stream);
+
+// Internal: fork onto / join back from the library's side stream (hip_context.hip).  Used to run independent
+// kernels of one launcher concurrently; legal inside stream capture.
+__attribute__((visibility("hidden"))) hipStream_t llmgen_fork_side_stream();
+__attribute__((visibility("hidden"))) void llmgen_join_side_stream(hipStream_t side);

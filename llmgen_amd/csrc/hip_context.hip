@@ -12,6 +12,8 @@
 
 hipStream_t g_llmgen_stream = nullptr;
 static bool g_own_stream = false;
+static hipStream_t g_side_stream = nullptr;
+static hipEvent_t g_fork_event = nullptr, g_join_event = nullptr;
 static hipGraph_t g_capture_graph = nullptr;
 
 #define HIP_WARN(call)                                                                                   \
@@ -19,6 +21,30 @@ static hipGraph_t g_capture_graph = nullptr;
         hipError_t e_ = (call);                                                                          \
         if (e_ != hipSuccess) fprintf(stderr, "[llmgen-hip] %s failed: %s\n", #call, hipGetErrorString(e_)); \
     } while (0)
+
+// Fork work onto the library's side stream after everything enqueued so far on the launch stream, and join it
+// back.  Both are event based, so they are legal inside stream capture (the side stream joins the capture).
+// Returns the side stream, or the launch stream itself if the side stream could not be created.
+hipStream_t llmgen_fork_side_stream() {
+    if (!g_side_stream) {
+        if (hipStreamCreateWithFlags(&g_side_stream, hipStreamNonBlocking) != hipSuccess ||
+            hipEventCreateWithFlags(&g_fork_event, hipEventDisableTiming) != hipSuccess ||
+            hipEventCreateWithFlags(&g_join_event, hipEventDisableTiming) != hipSuccess) {
+            g_side_stream = nullptr;
+            return g_llmgen_stream;
+        }
+    }
+    if (hipEventRecord(g_fork_event, g_llmgen_stream) != hipSuccess ||
+        hipStreamWaitEvent(g_side_stream, g_fork_event, 0) != hipSuccess)
+        return g_llmgen_stream;
+    return g_side_stream;
+}
+
+void llmgen_join_side_stream(hipStream_t side) {
+    if (side == g_llmgen_stream) return;
+    HIP_WARN(hipEventRecord(g_join_event, side));
+    HIP_WARN(hipStreamWaitEvent(g_llmgen_stream, g_join_event, 0));
+}
 
 extern "C" {
 

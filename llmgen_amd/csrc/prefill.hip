@@ -70,6 +70,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
     const int r0 = q0 + (wave & 1) * 32;  // first query row (within the segment) of this wave
     const int l32 = lane & 31, hh = lane >> 5;
 
+    if (q_len == 1) return;  // single-row segments (decode rows of a mixed step): streamed by the decode kernel
     if (ctx < q_len) {  // padding sequence: zero rows, no keys (cpu/attention.zig:80-83)
         const int row = r0 + l32;
         if (row < q_len) {
@@ -339,6 +340,11 @@ extern "C" void hip_attn_prefill(bf16_t *out, const bf16_t *q, const bf16_t *k_c
     // two waves per head; at most 8 waves (4 heads) per workgroup, the rest of the group in further workgroups
     const int heads_per_wg = G < 4 ? G : 4;
     const int head_groups = G / heads_per_wg;
+    // Decode rows (q_len == 1) go to the bandwidth-oriented decode kernel on the side stream, concurrently with
+    // the MFMA kernel (which skips them) on the launch stream: HBM-bound and MFMA-bound work overlap.
+    hipStream_t side = llmgen_fork_side_stream();
+    llmgen_decode_rows_of_prefill(out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq, n_tiles, nq,
+                                  nkv, max_blocks, block_size, scale, side);
     switch (heads_per_wg) {
         case 1: launch_prefill<2>(fast, head_groups, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq,
                                   tile_q0, n_tiles, nq, nkv, G, max_blocks, block_size, bs_shift, sl2); break;
@@ -347,4 +353,5 @@ extern "C" void hip_attn_prefill(bf16_t *out, const bf16_t *q, const bf16_t *k_c
         default: launch_prefill<8>(fast, head_groups, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq,
                                    tile_q0, n_tiles, nq, nkv, G, max_blocks, block_size, bs_shift, sl2); break;
     }
+    llmgen_join_side_stream(side);
 }

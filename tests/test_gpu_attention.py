@@ -161,3 +161,39 @@ def test_decode_graph_replays(gpu):
             run_gpu(make("kt_decode"), make("kt_decode").tensors(device="cuda"))
     finally:
         graphs.destroy()
+
+
+def test_mixed_step_graph_capture(gpu):
+    """A mixed prefill + decode-row step (two kernels on two streams, joined by events) recorded into a hip graph
+    and replayed three times with eager work in between; every replay matches the oracle."""
+    print("[gpu-test] mixed step graph capture", flush=True)
+    wl = make("gqa8")
+    t = wl.tensors(device="cuda")
+    pf = lib().hip_attn_prefill_tile()
+    meta = wl.meta(pf)
+    ws = A.Workspace.allocate(wl.nq, wl.hd, meta.n_seq, wl.max_model_len, meta_elems=meta.packed().size)
+    mgr = A.PagedAttentionManager()
+    mgr.layers[0] = A.LayerState(t["kc"].clone(), t["vc"].clone())
+    A.g_attn_mgr = mgr
+    A.bind_step(meta, ws, wl.nq, wl.nkv, wl.hd, wl.block_size, wl.max_blocks, wl.max_model_len)
+    out = torch.zeros((wl.n_tok, wl.nq, wl.hd), dtype=torch.bfloat16, device="cuda")
+    node = A.AttnNode(out, [t["q"], t["k"], t["v"]], layer_id=0)
+    A.PagedAttentionImpl.execute(0, node)  # warm-up (module load) outside capture
+    torch.cuda.synchronize()
+    L = lib()
+    assert L.hip_graph_begin() == 0
+    A.PagedAttentionImpl.execute(0, node)
+    g = L.hip_graph_end()
+    assert g, "capture failed"
+    _, _, _, of = run_oracle(wl, t)
+    try:
+        for i in range(3):
+            out.zero_()
+            L.hip_graph_launch(g)
+            torch.cuda.synchronize()
+            check_hip_error(f"mixed replay {i}")
+            compare(to_u16(out), of, f"mixed replay {i}")
+            run_gpu(make("kt_prefill"), make("kt_prefill").tensors(device="cuda"))  # eager work in between
+            A.g_attn_mgr = mgr
+    finally:
+        L.hip_graph_destroy(g)
