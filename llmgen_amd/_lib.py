@@ -61,9 +61,10 @@ def lib() -> ctypes.CDLL:
     global _lib
     if _lib is not None:
         return _lib
-    if not os.path.exists(LIB_PATH):
-        raise LibraryMissing(f"{LIB_PATH} is not built; run `python -m llmgen_amd.build` (hipcc, gfx950)")
-    handle = ctypes.CDLL(LIB_PATH)
+    path = os.environ.get("LLMGEN_ATTN_LIB", LIB_PATH)  # an alternative build of the same library (A/B runs)
+    if not os.path.exists(path):
+        raise LibraryMissing(f"{path} is not built; run `python -m llmgen_amd.build` (hipcc, gfx950)")
+    handle = ctypes.CDLL(path)
     for name, (res, args) in SIGNATURES.items():
         fn = getattr(handle, name)
         fn.restype = res

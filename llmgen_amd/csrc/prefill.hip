@@ -7,21 +7,24 @@
 // writes zeros.  The host tiles each segment into hip_attn_prefill_tile() rows (tile_seq, tile_q0).
 //
 // Design (one workgroup = one query tile x one KV head x a group of its G query heads):
+//   * K and V tiles of 64 keys move HBM -> LDS with global_load_lds_dwordx4 (no register staging, no VALU
+//     work): each wave instruction fills four 256-byte key rows.  Two LDS stages: tile t+1 streams in while
+//     tile t is computed, one barrier per tile.  Rows are stored as 16 chunks of 16 bytes with the chunk index
+//     XOR-swizzled by the row (K: row & 15, V: 2*row & 15) so the fragment reads below are bank-conflict free;
 //   * each wave owns 32 query rows of one head and computes S^T = K Q^T with v_mfma_f32_32x32x16_bf16: K
-//     (from LDS) is the A operand, Q (registers, loaded once) the B operand.  In the S^T accumulator layout
-//     every lane holds 32 keys of ONE query row, so the online softmax is lane-local except one exchange
-//     between the two half-waves;
-//   * the probabilities are rounded to bf16 in registers and used directly as the B operand of O^T = V^T P^T:
-//     the k-slots of that MFMA are assigned to keys in exactly the order the S^T accumulator holds them.  V^T
-//     comes from LDS, where the loader writes V transposed ([dim][key]) with keys permuted inside each group
-//     of 16 (bits 2 and 3 swapped) so each lane's 8 keys are one 16-byte ds_read;
-//   * K and V tiles of 64 keys are staged through LDS once per workgroup and shared by every wave (all G heads
-//     of the group and both row halves of the tile); the next tile's global loads are issued into registers
-//     before the current tile is computed;
-//   * online softmax in base 2 with scale * log2 e folded in, fp32 row state; causal masking only on tiles
-//     that cross a wave's diagonal; tiles wholly above a wave's diagonal are skipped by that wave;
+//     (ds_read_b128 from LDS) is the A operand, Q (registers, loaded once) the B operand.  In the S^T
+//     accumulator layout every lane holds 32 keys of ONE query row, so the online softmax is lane-local except
+//     one exchange between the two half-waves;
+//   * the probabilities are rounded to bf16 in registers and used directly as the B operand of O^T = V^T P^T
+//     (the MFMA's k-slots are assigned to keys in the order the S^T accumulator holds them).  The V^T A operand
+//     comes straight from the row-major V tile through ds_read_b64_tr_b16: a 16-lane group whose lane 4j+m
+//     addresses four dims of key j receives, in lane i, key j's value of dim i -- the transpose happens in the
+//     LDS read;
+//   * online softmax in base 2 with scale * log2 e folded in, fp32 row state, lazy rescaling (the reference max
+//     moves only when a row max grows by more than 2^8); causal masking only on tiles that cross a wave's
+//     diagonal; tiles wholly above a wave's diagonal are skipped by that wave;
 //   * grid is 1-D with the KV head fastest, so every workgroup of one KV head lands on the same XCD (8 XCDs,
-//     round-robin dispatch) and its K/V tiles stay in that XCD's L2; heavier (later) query tiles go first.
+//     round-robin dispatch) and its K/V tiles stay in that XCD's L2; later query tiles go first.
 #include "hip_common.h"
 
 #include <math.h>
@@ -31,13 +34,26 @@
 namespace {
 
 constexpr int HD = 128;
-constexpr int BQ = 64;            // query rows per tile (the value hip_attn_prefill_tile returns)
-constexpr int BK = 64;            // keys per LDS tile
-constexpr int KS_STRIDE = HD + 8;  // K tile row stride in bf16 (272 B: rows shift by 4 banks)
-constexpr int VT_STRIDE = BK + 8;  // V^T tile row stride in bf16 (144 B)
+constexpr int BQ = 64;               // query rows per tile (the value hip_attn_prefill_tile returns)
+constexpr int BK = 64;               // keys per LDS tile
+constexpr int TILE = BK * HD;        // bf16 elements of one K (or V) tile: 16 KB, rows of 256 B, no padding
 constexpr float RESCALE_LOG2 = 8.f;  // lazy-rescale threshold (log2 units)
 
-__device__ __forceinline__ int swap23(int b) { return (b & ~12) | ((b & 4) << 1) | ((b & 8) >> 1); }
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
+
+// element offset of (row, 16-byte chunk) in a swizzled tile
+__device__ __forceinline__ int k_off(int row, int chunk) { return row * HD + ((chunk ^ (row & 15)) << 3); }
+__device__ __forceinline__ int v_off(int row, int chunk) { return row * HD + ((chunk ^ ((row << 1) & 15)) << 3); }
+
+__device__ __forceinline__ s16x4_t ds_read_tr(const bf16_t *p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t *)p);
+}
+
+__device__ __forceinline__ void dma16(const bf16_t *gsrc, bf16_t *ldst) {
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)gsrc,
+                                     (__attribute__((address_space(3))) void *)ldst, 16, 0, 0);
+}
 
 // NW = waves per workgroup (2 per head: rows 0-31 and 32-63 of the tile); FAST = block_size is a power of two
 // and a multiple of BK (every K/V tile then lies inside one block).
@@ -49,13 +65,12 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
                         const int *__restrict__ tile_seq, const int *__restrict__ tile_q0, int n_tiles, int nq,
                         int nkv, int G, int head_groups, int max_blocks, int block_size, int bs_shift,
                         float scale_log2) {
-    constexpr int NT = 64 * NW;
-    constexpr int K_ITEMS = BK * (HD / 8) / NT;       // 16-byte K chunks per thread per tile
-    constexpr int V_ITEMS = (BK / 2) * (HD / 8) / NT;  // key pairs x 8 dims per thread per tile
-    static_assert(K_ITEMS >= 1 && V_ITEMS >= 1, "tile too small for the workgroup");
+    constexpr int LOADS = 16 / NW;  // 4-row DMA instructions per wave per tile, for K and for V each
 
-    __shared__ __attribute__((aligned(16))) bf16_t Ks[BK * KS_STRIDE];
-    __shared__ __attribute__((aligned(16))) bf16_t Vt[HD * VT_STRIDE];
+    __shared__ __attribute__((aligned(16))) bf16_t K0[TILE];
+    __shared__ __attribute__((aligned(16))) bf16_t V0[TILE];
+    __shared__ __attribute__((aligned(16))) bf16_t K1[TILE];
+    __shared__ __attribute__((aligned(16))) bf16_t V1[TILE];
 
     const int bid = blockIdx.x;
     const int kvh = bid % nkv;
@@ -71,7 +86,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
     const int l32 = lane & 31, hh = lane >> 5;
 
     if (q_len == 1) return;  // single-row segments (decode rows of a mixed step): streamed by the decode kernel
-    if (ctx < q_len) {  // padding sequence: zero rows, no keys (cpu/attention.zig:80-83)
+    if (ctx < q_len) {       // padding sequence: zero rows, no keys (cpu/attention.zig:80-83)
         const int row = r0 + l32;
         if (row < q_len) {
             bf16_t *o = out + ((long)(q_beg + row) * nq + head) * HD + hh * 64;
@@ -83,8 +98,8 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
     const int *bt = block_tables + (long)s * max_blocks;
     const long blk_stride = (long)nkv * block_size * HD;
     const long head_off = (long)kvh * block_size * HD;
-    const int base_pos = ctx - q_len;                          // position of segment row 0
-    const int kend = base_pos + min(q0 + BQ, q_len);            // keys needed by the whole tile
+    const int base_pos = ctx - q_len;                // position of segment row 0
+    const int kend = base_pos + min(q0 + BQ, q_len);  // keys needed by the whole tile
     const int n_iter = (kend + BK - 1) / BK;
 
     // ---- Q fragments (B operand): lane holds row r0+l32, dims c*16 + hh*8 .. +8 ----
@@ -103,85 +118,32 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
     const int wave_pos_max = base_pos + min(r0 + 31, q_len - 1);
     const bool wave_has_pad = r0 + 31 >= q_len;
 
-    // ---- global -> register prefetch of one K/V tile ----
-    u32x4_t kreg[K_ITEMS];
-    u32x4_t vreg[V_ITEMS][2];
-    auto prefetch = [&](int it) {
+    // ---- DMA of one K/V tile into (Kd, Vd): wave instruction i covers rows 4*(wave + NW*i) .. +3; lane writes
+    //      row + lane/16, physical chunk lane%16, so it reads the logical chunk that swizzles onto it ----
+    const int drow = lane >> 4, dchunk = lane & 15;
+    auto issue = [&](int it, bf16_t *Kd, bf16_t *Vd) {
         const int kb0 = it * BK;
+        const int last = kend - 1 - kb0;  // keys past kend reread the last valid key (finite data)
+        long kbase = 0;
         if (FAST) {
-            // block_size is a power of two and a multiple of BK, so the whole tile lies in one block: one
-            // scalar block-table read gives a scalar base, and every lane adds a 32-bit in-block offset
             const int phys = bt[__builtin_amdgcn_readfirstlane(kb0 >> bs_shift)];
-            const long base = (long)phys * blk_stride + head_off + (long)(kb0 & (block_size - 1)) * HD;
-            const bf16_t *kt = kc + base;
-            const bf16_t *vt = vc + base;
-            const int last = kend - 1 - kb0;  // clamp: keys past kend reread the last valid key
+            kbase = (long)phys * blk_stride + head_off + (long)(kb0 & (block_size - 1)) * HD;
+        }
 #pragma unroll
-            for (int i = 0; i < K_ITEMS; ++i) {
-                const int item = tid + i * NT;
-                kreg[i] = ld16(kt + min(item >> 4, last) * HD + (item & 15) * 8);
+        for (int i = 0; i < LOADS; ++i) {
+            const int rbase = 4 * (wave + NW * i);
+            const int r = rbase + drow;
+            const int key = min(r, last);
+            long src;
+            if (FAST) {
+                src = kbase + (long)key * HD;
+            } else {
+                const int t = kb0 + key;
+                const int bi = t / block_size;
+                src = (long)bt[bi] * blk_stride + head_off + (long)(t - bi * block_size) * HD;
             }
-#pragma unroll
-            for (int i = 0; i < V_ITEMS; ++i) {
-                const int item = tid + i * NT;
-                const int kp = item & 31, dc = item >> 5;
-                vreg[i][0] = ld16(vt + min(2 * kp, last) * HD + dc * 8);
-                vreg[i][1] = ld16(vt + min(2 * kp + 1, last) * HD + dc * 8);
-            }
-            return;
-        }
-        int kkey[K_ITEMS], vkey[V_ITEMS][2], kblk[K_ITEMS], vblk[V_ITEMS][2];
-#pragma unroll
-        for (int i = 0; i < K_ITEMS; ++i) kkey[i] = min(kb0 + ((tid + i * NT) >> 4), kend - 1);
-#pragma unroll
-        for (int i = 0; i < V_ITEMS; ++i) {
-            const int kp = (tid + i * NT) & 31;
-            vkey[i][0] = min(kb0 + 2 * kp, kend - 1);
-            vkey[i][1] = min(kb0 + 2 * kp + 1, kend - 1);
-        }
-        // generic block size: independent block-table reads first, then the K/V reads
-#pragma unroll
-        for (int i = 0; i < K_ITEMS; ++i) kblk[i] = bt[kkey[i] / block_size];
-#pragma unroll
-        for (int i = 0; i < V_ITEMS; ++i)
-#pragma unroll
-            for (int e = 0; e < 2; ++e) vblk[i][e] = bt[vkey[i][e] / block_size];
-#pragma unroll
-        for (int i = 0; i < K_ITEMS; ++i) {
-            const int off = kkey[i] % block_size;
-            kreg[i] = ld16(kc + (long)kblk[i] * blk_stride + head_off + (long)off * HD + ((tid + i * NT) & 15) * 8);
-        }
-#pragma unroll
-        for (int i = 0; i < V_ITEMS; ++i) {
-            const int dc = (tid + i * NT) >> 5;
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                const int off = vkey[i][e] % block_size;
-                vreg[i][e] = ld16(vc + (long)vblk[i][e] * blk_stride + head_off + (long)off * HD + dc * 8);
-            }
-        }
-    };
-    auto commit = [&]() {
-#pragma unroll
-        for (int i = 0; i < K_ITEMS; ++i) {
-            const int item = tid + i * NT;
-            *reinterpret_cast<u32x4_t *>(Ks + (item >> 4) * KS_STRIDE + (item & 15) * 8) = kreg[i];
-        }
-#pragma unroll
-        for (int i = 0; i < V_ITEMS; ++i) {
-            const int item = tid + i * NT;
-            const int kp = item & 31, dc = item >> 5;
-            const int key0 = 2 * kp;
-            const int pos = (key0 & ~15) | swap23(key0 & 15);
-            bf16_t *dst = Vt + (dc * 8) * VT_STRIDE + pos;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint32_t a = vreg[i][0][j], b = vreg[i][1][j];
-                // dims 2j and 2j+1: (key0, key0+1) pairs of bf16 -> one dword per dim row
-                *reinterpret_cast<uint32_t *>(dst + (2 * j) * VT_STRIDE) = __builtin_amdgcn_perm(b, a, 0x05040100u);
-                *reinterpret_cast<uint32_t *>(dst + (2 * j + 1) * VT_STRIDE) =
-                    __builtin_amdgcn_perm(b, a, 0x07060302u);
-            }
+            dma16(kc + src + ((dchunk ^ (r & 15)) << 3), Kd + rbase * HD);
+            dma16(vc + src + ((dchunk ^ ((r << 1) & 15)) << 3), Vd + rbase * HD);
         }
     };
 
@@ -192,19 +154,32 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
         for (int r = 0; r < 16; ++r) o[db][r] = 0.f;
     float m_run = -INFINITY, l_run = 0.f;
 
+    // per-lane LDS offsets of the V^T fragment reads (ds_read_b64_tr_b16): 16-lane group g4, lane i = 4j + m;
+    // the fragment's k-slots (hh*8 + e) are keys kc16*16 + (e/4)*8 + hh*4 + e%4, so the two reads of a fragment
+    // take keys hh*4 + j (+8) and dims db*32 + (g4&1)*16 + 4m .. +3
+    int voff[4];
+    {
+        const int g4 = lane >> 4, i = lane & 15, j = i >> 2, m = i & 3;
+        const int key = (g4 >> 1) * 4 + j;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+            const int dim = db * 32 + (g4 & 1) * 16 + 4 * m;
+            voff[db] = v_off(key, dim >> 3) + (dim & 7);
+        }
+    }
+
     // One 64-key tile for this wave: S^T = K Q^T, online softmax (base 2, scale folded into one FMA), O^T += V^T P^T.
-    auto tile_step = [&](int kb0, auto masked) {
+    auto tile_step = [&](int kb0, const bf16_t *Ks, const bf16_t *Vs, auto masked) {
         constexpr bool MASK = decltype(masked)::value;
         f32x16_t sacc[2];
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
             for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
-        const bf16_t *kp = Ks + l32 * KS_STRIDE + hh * 8;
 #pragma unroll
         for (int c = 0; c < 8; ++c) {  // two independent accumulation chains interleaved
-            const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t *>(kp + c * 16);
-            const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t *>(kp + 32 * KS_STRIDE + c * 16);
+            const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t *>(Ks + k_off(l32, 2 * c + hh));
+            const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t *>(Ks + k_off(32 + l32, 2 * c + hh));
             sacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qf[c], sacc[0], 0, 0, 0);
             sacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qf[c], sacc[1], 0, 0, 0);
         }
@@ -221,8 +196,6 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
                 mx = fmaxf(mx, sacc[kb][r]);
             }
         mx = fmaxf(mx, lane_xor(mx, 32)) * scale_log2;  // scale > 0 commutes with max
-        // Lazy rescaling: the reference max m_run only moves when a row's max exceeds it by more than
-        // RESCALE_LOG2 (or on the first keys), so the o rescale below is rare; probabilities stay <= 2^8.
         const bool grow = mx > m_run + RESCALE_LOG2;
         const float m_new = grow ? mx : m_run;
         const float m_use = (MASK && m_new == -INFINITY) ? 0.f : m_new;
@@ -230,20 +203,19 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
         float lsum = 0.f;
         bf16x8_t pf[4];  // B fragments for the four 16-key steps of P V
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+        for (int kc16 = 0; kc16 < 4; ++kc16) {
+            const int kb = kc16 >> 1, half = kc16 & 1;
+            float p[8];
 #pragma unroll
-            for (int half = 0; half < 2; ++half) {
-                float p[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    p[e] = fast_exp2(__builtin_fmaf(sacc[kb][half * 8 + e], scale_log2, -m_use));
-                    lsum += p[e];
-                }
-                u32x4_t w;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) w[e] = pack_bf16x2(p[2 * e], p[2 * e + 1]);
-                pf[kb * 2 + half] = __builtin_bit_cast(bf16x8_t, w);
+            for (int e = 0; e < 8; ++e) {
+                p[e] = fast_exp2(__builtin_fmaf(sacc[kb][half * 8 + e], scale_log2, -m_use));
+                lsum += p[e];
             }
+            u32x4_t w;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) w[e] = pack_bf16x2(p[2 * e], p[2 * e + 1]);
+            pf[kc16] = __builtin_bit_cast(bf16x8_t, w);
+        }
         l_run = l_run * corr + lsum;
         m_run = m_new;
         if (__any(grow)) {  // corr == 1 in rows that did not move
@@ -253,31 +225,43 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
                 for (int r = 0; r < 16; ++r) o[db][r] *= corr;
         }
         // ---- O^T[dim][row] += V^T P^T: four independent accumulators per 16-key step ----
-        const bf16_t *vp = Vt + l32 * VT_STRIDE + hh * 8;
 #pragma unroll
         for (int kc16 = 0; kc16 < 4; ++kc16)
 #pragma unroll
             for (int db = 0; db < 4; ++db) {
-                const bf16x8_t a = *reinterpret_cast<const bf16x8_t *>(vp + db * 32 * VT_STRIDE + kc16 * 16);
+                const bf16_t *vp = Vs + kc16 * 16 * HD + voff[db];
+                const s16x4_t lo = ds_read_tr(vp);           // keys hh*4 + j
+                const s16x4_t hi = ds_read_tr(vp + 8 * HD);  // keys 8 + hh*4 + j
+                const bf16x8_t a = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
                 o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pf[kc16], o[db], 0, 0, 0);
             }
     };
-
-    if (n_iter > 0) prefetch(0);
-    for (int it = 0; it < n_iter; ++it) {
+    auto compute = [&](int it, const bf16_t *Ks, const bf16_t *Vs) {
         const int kb0 = it * BK;
-        __syncthreads();  // every wave is done reading the previous tile
-        commit();
-        __syncthreads();
-        if (it + 1 < n_iter) prefetch(it + 1);
-
         if (wave_active && kb0 <= wave_pos_max) {
             // tiles wholly below the wave's diagonal (and with no padding rows) take the unmasked path
             if (wave_has_pad || kb0 + BK - 1 > wave_pos_min)
-                tile_step(kb0, std::true_type{});
+                tile_step(kb0, Ks, Vs, std::true_type{});
             else
-                tile_step(kb0, std::false_type{});
+                tile_step(kb0, Ks, Vs, std::false_type{});
         }
+    };
+
+    // two LDS stages; the loop is unrolled twice so every DMA targets a fixed buffer (the compiler can then see
+    // that the reads of one stage never wait for the DMA into the other)
+    if (n_iter > 0) issue(0, K0, V0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (int it = 0; it < n_iter; it += 2) {
+        if (it + 1 < n_iter) issue(it + 1, K1, V1);
+        compute(it, K0, V0);
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA into stage 1 has landed
+        __syncthreads();                // ... and everyone's; everyone is done reading stage 0
+        if (it + 1 >= n_iter) break;
+        if (it + 2 < n_iter) issue(it + 2, K0, V0);
+        compute(it + 1, K1, V1);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
     }
 
     // ---- normalise and store: lane holds dims db*32 + (r/4)*8 + hh*4 + r%4 of row my_row ----
@@ -298,9 +282,9 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
 }
 
 template <int NW>
-void launch_prefill(bool fast, int head_groups, bf16_t *out, const bf16_t *q, const bf16_t *kc, const bf16_t *vc, const int *bt,
-                    const int *ctx, const int *cu_q, const int *tile_seq, const int *tile_q0, int n_tiles, int nq,
-                    int nkv, int G, int max_blocks, int block_size, int bs_shift, float sl2) {
+void launch_prefill(bool fast, int head_groups, bf16_t *out, const bf16_t *q, const bf16_t *kc, const bf16_t *vc,
+                    const int *bt, const int *ctx, const int *cu_q, const int *tile_seq, const int *tile_q0,
+                    int n_tiles, int nq, int nkv, int G, int max_blocks, int block_size, int bs_shift, float sl2) {
     const long grid = (long)n_tiles * nkv * head_groups;
     if (fast)
         hipLaunchKernelGGL((attn_prefill_kernel<NW, true>), dim3((unsigned)grid), dim3(64 * NW), 0, g_llmgen_stream,
