@@ -10,7 +10,7 @@
 //   * K and V tiles of 64 keys move HBM -> LDS with global_load_lds_dwordx4 (no register staging, no VALU
 //     work): each wave instruction fills four 256-byte key rows.  Two LDS stages: tile t+1 streams in while
 //     tile t is computed, one barrier per tile.  Rows are stored as 16 chunks of 16 bytes with the chunk index
-//     XOR-swizzled by the row (K: row & 15, V: 2*row & 15) so the fragment reads below are bank-conflict free;
+//     XOR-swizzled by the row (K: row & 15, V: 4*row & 15) so the fragment reads below are bank-conflict free;
 //   * each wave owns 32 query rows of one head and computes S^T = K Q^T with v_mfma_f32_32x32x16_bf16: K
 //     (ds_read_b128 from LDS) is the A operand, Q (registers, loaded once) the B operand.  In the S^T
 //     accumulator layout every lane holds 32 keys of ONE query row, so the online softmax is lane-local except
@@ -44,7 +44,7 @@ typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
 
 // element offset of (row, 16-byte chunk) in a swizzled tile
 __device__ __forceinline__ int k_off(int row, int chunk) { return row * HD + ((chunk ^ (row & 15)) << 3); }
-__device__ __forceinline__ int v_off(int row, int chunk) { return row * HD + ((chunk ^ ((row << 1) & 15)) << 3); }
+__device__ __forceinline__ int v_off(int row, int chunk) { return row * HD + ((chunk ^ ((row << 2) & 15)) << 3); }
 
 __device__ __forceinline__ s16x4_t ds_read_tr(const bf16_t *p) {
     return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t *)p);
@@ -143,7 +143,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
                 src = (long)bt[bi] * blk_stride + head_off + (long)(t - bi * block_size) * HD;
             }
             dma16(kc + src + ((dchunk ^ (r & 15)) << 3), Kd + rbase * HD);
-            dma16(vc + src + ((dchunk ^ ((r << 1) & 15)) << 3), Vd + rbase * HD);
+            dma16(vc + src + ((dchunk ^ ((r << 2) & 15)) << 3), Vd + rbase * HD);
         }
     };
 
@@ -168,6 +168,12 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
         }
     }
 
+    // per-lane LDS offsets of the K fragment reads (row l32, logical chunk 2c + hh); row 32 + l32 has the same
+    // swizzle, so its offset is a constant 32 rows further
+    int koff[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) koff[c] = k_off(l32, 2 * c + hh);
+
     // One 64-key tile for this wave: S^T = K Q^T, online softmax (base 2, scale folded into one FMA), O^T += V^T P^T.
     auto tile_step = [&](int kb0, const bf16_t *Ks, const bf16_t *Vs, auto masked) {
         constexpr bool MASK = decltype(masked)::value;
@@ -178,8 +184,8 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
             for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
 #pragma unroll
         for (int c = 0; c < 8; ++c) {  // two independent accumulation chains interleaved
-            const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t *>(Ks + k_off(l32, 2 * c + hh));
-            const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t *>(Ks + k_off(32 + l32, 2 * c + hh));
+            const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t *>(Ks + koff[c]);
+            const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t *>(Ks + koff[c] + 32 * HD);
             sacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qf[c], sacc[0], 0, 0, 0);
             sacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qf[c], sacc[1], 0, 0, 0);
         }
