@@ -1,4 +1,4 @@
-"""ctypes binding of libllmgen_attn.so (the C-ABI declared in include/llmgen_attn.h).
+"""ctypes binding of libllmgen_attn.so (the C-ABI declared in include/llmgen_attn.h and include/llmgen_model.h).
 
 The library is loaded from the package directory (built in-tree by ``llmgen_amd.build``).  There is no fallback:
 if the library is missing or fails to load, :func:`lib` raises, so nothing on the product path can silently run
@@ -15,8 +15,9 @@ _P = ctypes.c_void_p
 _I = ctypes.c_int
 _F = ctypes.c_float
 _SZ = ctypes.c_size_t
+_L = ctypes.c_long
 
-# name -> (restype, argtypes); must match include/llmgen_attn.h
+# name -> (restype, argtypes); must match include/llmgen_attn.h and include/llmgen_model.h
 SIGNATURES = {
     "hip_store_kv": (None, [_P, _P, _P, _P, _P, _I, _I, _I, _I]),
     "hip_attn_decode": (None, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P, _P, _I, _I]),
@@ -47,6 +48,17 @@ SIGNATURES = {
     "hip_timer_record": (None, [_P]),
     "hip_timer_elapsed_ms": (_F, [_P, _P]),
     "hip_timer_destroy": (None, [_P]),
+    # include/llmgen_model.h
+    "hip_embedding": (None, [_P, _P, _P, _I, _I]),
+    "hip_rmsnorm": (None, [_P, _P, _P, _L, _I, _F]),
+    "hip_linear": (None, [_P, _I, _P, _P, _I, _I, _I]),
+    "hip_rope": (None, [_P, _P, _P, _P, _P, _I, _I, _I]),
+    "hip_silu": (None, [_P, _P, _SZ]),
+    "hip_add": (None, [_P, _P, _P, _SZ]),
+    "hip_mul": (None, [_P, _P, _P, _SZ]),
+    "hip_gather_rows": (None, [_P, _P, _P, _I, _I]),
+    "hip_sample": (None, [_P, _P, _P, _P, _I, _I, _P]),
+    "hip_sample_scratch_bytes": (_SZ, [_I]),
 }
 
 _lib = None

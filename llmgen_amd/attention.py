@@ -19,6 +19,7 @@ import math
 from dataclasses import dataclass, field
 from typing import Dict, List, Optional
 
+import numpy as np
 import torch
 
 from . import step as stepmod
@@ -52,6 +53,7 @@ class StepState:
     block_size: int = 0
     max_blocks: int = 0
     max_model_len: int = 0
+    pos: int = 0
     slots: int = 0
     cu_q: int = 0
     ctx: int = 0
@@ -182,9 +184,9 @@ def bind_step(meta: "stepmod.StepMeta", ws: Workspace, nq: int, nkv: int, hd: in
     g = g_step
     g.n_tok, g.n_seq, g.n_tiles, g.decode = meta.n_tok, meta.n_seq, meta.n_tiles, meta.decode
     g.n_head, g.n_kv_head, g.head_dim = nq, nkv, hd
-    g.attn_scale = 1.0 / math.sqrt(hd)
+    g.attn_scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))  # f32, as executor.zig:877
     g.block_size, g.max_blocks, g.max_model_len = block_size, max_blocks, max_model_len
-    for name in ("slots", "cu_q", "ctx", "last", "tile_seq", "tile_q0", "block_tables"):
+    for name in ("pos", "slots", "cu_q", "ctx", "last", "tile_seq", "tile_q0", "block_tables"):
         setattr(g, name, base + 4 * off[name])
     g.part_o, g.part_ml = ws.part_o.data_ptr(), ws.part_ml.data_ptr()
     return g

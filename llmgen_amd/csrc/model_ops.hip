@@ -1,0 +1,335 @@
+// model_ops.hip -- the non-attention ops of the Qwen3 forward (embedding, RMSNorm, linear, NEOX RoPE, SiLU,
+// add, mul, gather_last, sampling) for the end-to-end greedy-token check.
+//
+// These kernels trade speed for reproducibility: every output is computed in the order the reference CPU
+// backend uses (src/backend/cpu/*.zig), with one IEEE rounding per f32 multiply / add / divide / sqrt and one
+// RNE rounding to bf16 per stored value, so a forward built from them matches the CPU backend bit for bit
+// outside attention.  Contraction into FMAs is switched off for the whole file for that reason.  They are not
+// part of the measured hot path.
+#include "hip_common.h"
+
+#include <math.h>
+
+#pragma clang fp contract(off)
+
+namespace {
+
+__device__ __forceinline__ float bf2f(bf16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
+__device__ __forceinline__ bf16_t f2bf(float f) { return __builtin_bit_cast(bf16_t, (__bf16)f); }
+
+// ---------------------------------------------------------------------------------------------- embedding
+__global__ void embedding_kernel(bf16_t *out, const int *ids, const bf16_t *w, int T, int H) {
+    const int chunks = H >> 3;
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long)T * chunks) return;
+    const int t = (int)(i / chunks), c = (int)(i % chunks);
+    const long row = ids[t];
+    *reinterpret_cast<u32x4_t *>(out + (long)t * H + c * 8) = ld16(w + row * H + c * 8);
+}
+
+// ---------------------------------------------------------------------------------------------- RMSNorm
+// One wave per row.  The row is staged in LDS as f32; lane 0 forms the sum of squares in index order (the
+// reference's order), the wave then writes bf16(bf16(x * scale) * w).
+constexpr int NORM_MAX_D = 8192;
+__global__ void __launch_bounds__(64) rmsnorm_kernel(bf16_t *out, const bf16_t *x, const float *w, int D,
+                                                      float eps) {
+    __shared__ float row[NORM_MAX_D];
+    __shared__ float scale_s;
+    const long r = blockIdx.x;
+    const bf16_t *xr = x + r * D;
+    for (int c = threadIdx.x; c < (D >> 3); c += 64) {
+        float f[8];
+        unpack_bf16x8(ld16(xr + c * 8), f);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) row[c * 8 + j] = f[j];
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float ss = 0.0f;
+        for (int h = 0; h < D; ++h) ss += row[h] * row[h];
+        scale_s = 1.0f / sqrtf(ss / (float)D + eps);
+    }
+    __syncthreads();
+    const float scale = scale_s;
+    for (int h = threadIdx.x; h < D; h += 64) {
+        const float normed = bf2f(f2bf(row[h] * scale));
+        out[r * D + h] = f2bf(normed * w[h]);
+    }
+}
+
+// ---------------------------------------------------------------------------------------------- linear
+// y[m][n] = sum_k x[m][k] * w[n][k], k ascending.  A workgroup owns 256 output columns (one per thread) and
+// LIN_MB rows; K advances in tiles of LIN_KT: the W tile (256 x LIN_KT bf16) and the x tile (LIN_MB x LIN_KT,
+// as f32) are staged in LDS with coalesced 16-byte loads.  W rows are padded to an odd number of dwords so the
+// 64 lanes of a wave read 64 different banks.  Each thread keeps LIN_MB independent chains.
+constexpr int LIN_N = 256, LIN_MB = 8, LIN_KT = 32;
+constexpr int LIN_WSTRIDE = LIN_KT / 2 + 1;  // dwords per padded W row (17)
+
+__global__ void __launch_bounds__(LIN_N) linear_kernel(void *y, int y_f32, const bf16_t *x, const bf16_t *w, int M,
+                                                       int N, int K) {
+    __shared__ uint32_t ws[LIN_N * LIN_WSTRIDE];
+    __shared__ float xs[LIN_MB][LIN_KT];
+    const int tid = threadIdx.x;
+    const int n0 = blockIdx.x * LIN_N, m0 = blockIdx.y * LIN_MB;
+    const int n = n0 + tid;
+    const int mrows = min(LIN_MB, M - m0);
+    float acc[LIN_MB];
+#pragma unroll
+    for (int m = 0; m < LIN_MB; ++m) acc[m] = 0.0f;
+
+    for (int k0 = 0; k0 < K; k0 += LIN_KT) {
+        const int kt = min(LIN_KT, K - k0);  // multiple of 8
+        // W tile: 256 rows x (kt / 8) chunks of 16 bytes
+        for (int i = tid; i < LIN_N * (LIN_KT / 8); i += LIN_N) {
+            const int r = i / (LIN_KT / 8), c = i % (LIN_KT / 8);
+            u32x4_t v = {0u, 0u, 0u, 0u};
+            if (n0 + r < N && c * 8 < kt) v = ld16(w + (long)(n0 + r) * K + k0 + c * 8);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) ws[r * LIN_WSTRIDE + c * 4 + j] = v[j];
+        }
+        // x tile: mrows x (kt / 8) chunks
+        for (int i = tid; i < LIN_MB * (LIN_KT / 8); i += LIN_N) {
+            const int r = i / (LIN_KT / 8), c = i % (LIN_KT / 8);
+            float f[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            if (r < mrows && c * 8 < kt) unpack_bf16x8(ld16(x + (long)(m0 + r) * K + k0 + c * 8), f);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) xs[r][c * 8 + j] = f[j];
+        }
+        __syncthreads();
+        for (int kk = 0; kk < kt; kk += 2) {
+            const uint32_t wp = ws[tid * LIN_WSTRIDE + (kk >> 1)];
+            const float w0 = bf16lo_to_f32(wp), w1 = bf16hi_to_f32(wp);
+#pragma unroll
+            for (int m = 0; m < LIN_MB; ++m) {
+                acc[m] = acc[m] + xs[m][kk] * w0;
+                acc[m] = acc[m] + xs[m][kk + 1] * w1;
+            }
+        }
+        __syncthreads();
+    }
+    if (n >= N) return;
+    for (int m = 0; m < mrows; ++m) {
+        const long o = (long)(m0 + m) * N + n;
+        if (y_f32)
+            static_cast<float *>(y)[o] = acc[m];
+        else
+            static_cast<bf16_t *>(y)[o] = f2bf(acc[m]);
+    }
+}
+
+// ---------------------------------------------------------------------------------------------- RoPE
+__global__ void rope_kernel(bf16_t *out, const bf16_t *x, const float *cos_t, const float *sin_t, const int *pos,
+                            int T, int n_head, int hd) {
+    const int half = hd >> 1;
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long)T * n_head * half) return;
+    const int d = (int)(i % half);
+    const long th = i / half;  // t * n_head + h
+    const int t = (int)(th / n_head);
+    const long b = th * hd;
+    const long p = pos[t];
+    const float c = cos_t[p * hd + d], s = sin_t[p * hd + d];
+    const float x0 = bf2f(x[b + d]), x1 = bf2f(x[b + d + half]);
+    out[b + d] = f2bf(x0 * c - x1 * s);
+    out[b + d + half] = f2bf(x1 * c + x0 * s);
+}
+
+// ---------------------------------------------------------------------------------------------- elementwise
+// exp in double, rounded once to f32: the correctly rounded f32 exp except in vanishingly rare double-rounding
+// cases, which is what a correctly rounded host expf returns.
+__global__ void silu_kernel(bf16_t *out, const bf16_t *x, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float v = bf2f(x[i]);
+    const float e = (float)exp(-(double)v);
+    out[i] = f2bf(v / (1.0f + e));
+}
+
+__global__ void add_kernel(bf16_t *out, const bf16_t *a, const bf16_t *b, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = f2bf(bf2f(a[i]) + bf2f(b[i]));
+}
+
+__global__ void mul_kernel(bf16_t *out, const bf16_t *a, const bf16_t *b, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = f2bf(bf2f(a[i]) * bf2f(b[i]));
+}
+
+__global__ void gather_rows_kernel(bf16_t *out, const bf16_t *x, const int *idx, int S, int H) {
+    const int chunks = H >> 3;
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long)S * chunks) return;
+    const int s = (int)(i / chunks), c = (int)(i % chunks);
+    *reinterpret_cast<u32x4_t *>(out + (long)s * H + c * 8) = ld16(x + (long)idx[s] * H + c * 8);
+}
+
+// ---------------------------------------------------------------------------------------------- sampling
+// Phase 1: grid (S, SAMPLE_SPLIT); each workgroup finds (max, first index) over one contiguous chunk of the row.
+// Phase 2: one wave per row merges the SAMPLE_SPLIT candidates.  Merging keeps the larger value and, on equal
+// values, the smaller index, which is the reference's sequential "strictly greater" scan.  NaN never wins
+// (every comparison with it is false), as in the scan.  A row with no candidate (all -inf / NaN) yields 0.
+constexpr int SAMPLE_SPLIT = 32, SAMPLE_THREADS = 256;
+constexpr int NO_INDEX = 0x7fffffff;
+
+__device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
+    x += 0x9E3779B97F4A7C15ull;
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+    return x ^ (x >> 31);
+}
+
+__device__ __forceinline__ void argmax_merge(float &bv, int &bi, float v, int i) {
+    if (v > bv || (v == bv && i < bi)) {
+        bv = v;
+        bi = i;
+    }
+}
+
+__device__ __forceinline__ void wave_argmax(float &bv, int &bi) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        const float ov = lane_xor(bv, m);
+        const int oi = __builtin_bit_cast(int, lane_xor(__builtin_bit_cast(float, bi), m));
+        argmax_merge(bv, bi, ov, oi);
+    }
+}
+
+__global__ void __launch_bounds__(SAMPLE_THREADS) sample_partial_kernel(float *pv, int *pi, const bf16_t *logits,
+                                                                        const float *temps, const uint64_t *seed,
+                                                                        int V) {
+    const int s = blockIdx.x, part = blockIdx.y;
+    const int chunk = (V + SAMPLE_SPLIT - 1) / SAMPLE_SPLIT;
+    const int beg = part * chunk, end = min(V, beg + chunk);
+    const bf16_t *row = logits + (long)s * V;
+    const float temp = temps[s];
+    float bv = -INFINITY;
+    int bi = NO_INDEX;
+    if (temp > 0.0f) {
+        const uint64_t rs = splitmix64(*seed ^ ((uint64_t)s << 40));
+        for (int i = beg + threadIdx.x; i < end; i += SAMPLE_THREADS) {
+            const uint64_t r = splitmix64(rs + (uint64_t)i);
+            const float u = ((float)(r >> 40) + 0.5f) * (1.0f / 16777216.0f);
+            argmax_merge(bv, bi, bf2f(row[i]) / temp - logf(-logf(u)), i);
+        }
+    } else {
+        for (int i = beg + threadIdx.x; i < end; i += SAMPLE_THREADS) argmax_merge(bv, bi, bf2f(row[i]), i);
+    }
+    wave_argmax(bv, bi);
+    __shared__ float sv[SAMPLE_THREADS / 64];
+    __shared__ int si[SAMPLE_THREADS / 64];
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        sv[wave] = bv;
+        si[wave] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w2 = 1; w2 < SAMPLE_THREADS / 64; ++w2) argmax_merge(bv, bi, sv[w2], si[w2]);
+        pv[s * SAMPLE_SPLIT + part] = bv;
+        pi[s * SAMPLE_SPLIT + part] = bi;
+    }
+}
+
+__global__ void __launch_bounds__(64) sample_final_kernel(int *out, const float *pv, const int *pi) {
+    const int s = blockIdx.x, lane = threadIdx.x;
+    float bv = lane < SAMPLE_SPLIT ? pv[s * SAMPLE_SPLIT + lane] : -INFINITY;
+    int bi = lane < SAMPLE_SPLIT ? pi[s * SAMPLE_SPLIT + lane] : NO_INDEX;
+    wave_argmax(bv, bi);
+    if (lane == 0) out[s] = bi == NO_INDEX ? 0 : bi;
+}
+
+bool reject(const char *what) {
+    fprintf(stderr, "llmgen: %s\n", what);
+    return true;
+}
+
+unsigned blocks_for(size_t n, unsigned per) { return (unsigned)((n + per - 1) / per); }
+
+}  // namespace
+
+extern "C" {
+
+void hip_embedding(uint16_t *out, const int32_t *ids, const uint16_t *weight, int T, int H) {
+    if (T <= 0) return;
+    if (H <= 0 || H % 8 != 0) {
+        reject("hip_embedding: H must be a positive multiple of 8");
+        return;
+    }
+    const size_t n = (size_t)T * (H / 8);
+    embedding_kernel<<<blocks_for(n, 256), 256, 0, g_llmgen_stream>>>(out, ids, weight, T, H);
+}
+
+void hip_rmsnorm(uint16_t *out, const uint16_t *x, const float *w, long rows, int D, float eps) {
+    if (rows <= 0) return;
+    if (D <= 0 || D % 8 != 0 || D > NORM_MAX_D) {
+        reject("hip_rmsnorm: D must be a positive multiple of 8, at most 8192");
+        return;
+    }
+    rmsnorm_kernel<<<(unsigned)rows, 64, 0, g_llmgen_stream>>>(out, x, w, D, eps);
+}
+
+void hip_linear(void *y, int y_f32, const uint16_t *x, const uint16_t *w, int M, int N, int K) {
+    if (M <= 0 || N <= 0) return;
+    if (K <= 0 || K % 8 != 0) {
+        reject("hip_linear: K must be a positive multiple of 8");
+        return;
+    }
+    const dim3 grid((N + LIN_N - 1) / LIN_N, (M + LIN_MB - 1) / LIN_MB);
+    linear_kernel<<<grid, LIN_N, 0, g_llmgen_stream>>>(y, y_f32, x, w, M, N, K);
+}
+
+void hip_rope(uint16_t *out, const uint16_t *x, const float *cos_tab, const float *sin_tab, const int32_t *positions,
+              int T, int n_head, int hd) {
+    if (T <= 0 || n_head <= 0) return;
+    if (hd <= 0 || hd % 2 != 0) {
+        reject("hip_rope: hd must be positive and even");
+        return;
+    }
+    const size_t n = (size_t)T * n_head * (hd / 2);
+    rope_kernel<<<blocks_for(n, 256), 256, 0, g_llmgen_stream>>>(out, x, cos_tab, sin_tab, positions, T, n_head, hd);
+}
+
+void hip_silu(uint16_t *out, const uint16_t *x, size_t n) {
+    if (n == 0) return;
+    silu_kernel<<<blocks_for(n, 256), 256, 0, g_llmgen_stream>>>(out, x, n);
+}
+
+void hip_add(uint16_t *out, const uint16_t *a, const uint16_t *b, size_t n) {
+    if (n == 0) return;
+    add_kernel<<<blocks_for(n, 256), 256, 0, g_llmgen_stream>>>(out, a, b, n);
+}
+
+void hip_mul(uint16_t *out, const uint16_t *a, const uint16_t *b, size_t n) {
+    if (n == 0) return;
+    mul_kernel<<<blocks_for(n, 256), 256, 0, g_llmgen_stream>>>(out, a, b, n);
+}
+
+void hip_gather_rows(uint16_t *out, const uint16_t *x, const int32_t *idx, int S, int H) {
+    if (S <= 0) return;
+    if (H <= 0 || H % 8 != 0) {
+        reject("hip_gather_rows: H must be a positive multiple of 8");
+        return;
+    }
+    const size_t n = (size_t)S * (H / 8);
+    gather_rows_kernel<<<blocks_for(n, 256), 256, 0, g_llmgen_stream>>>(out, x, idx, S, H);
+}
+
+size_t hip_sample_scratch_bytes(int max_S) {
+    return max_S <= 0 ? 0 : (size_t)max_S * SAMPLE_SPLIT * (sizeof(float) + sizeof(int));
+}
+
+void hip_sample(int32_t *out_ids, const uint16_t *logits, const float *temps, const uint64_t *seed, int S, int V,
+                void *scratch) {
+    if (S <= 0) return;
+    if (V <= 0 || scratch == nullptr) {
+        reject("hip_sample: V must be positive and scratch non-null");
+        return;
+    }
+    float *pv = static_cast<float *>(scratch);
+    int *pi = reinterpret_cast<int *>(pv + (size_t)S * SAMPLE_SPLIT);
+    sample_partial_kernel<<<dim3(S, SAMPLE_SPLIT), SAMPLE_THREADS, 0, g_llmgen_stream>>>(pv, pi, logits, temps, seed,
+                                                                                         V);
+    sample_final_kernel<<<S, 64, 0, g_llmgen_stream>>>(out_ids, pv, pi);
+}
+
+}  // extern "C"

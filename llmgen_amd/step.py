@@ -82,12 +82,14 @@ class StepMeta:
     tile_seq: np.ndarray
     tile_q0: np.ndarray
     block_tables: np.ndarray  # [n_seq, max_blocks]
+    pos: Optional[np.ndarray] = None  # [n_tok] position of each token in its sequence (padding rows: 0)
     offsets: dict = field(default_factory=dict)
 
     def packed(self) -> np.ndarray:
-        """One contiguous int32 buffer in Layout order (executor.zig:139-202, without ids/pos/temps/seed, which
+        """One contiguous int32 buffer in Layout order (executor.zig:139-202, without ids/temps/seed, which
         attention does not read); offsets (in int32 elements) are recorded in ``self.offsets``."""
-        parts = [("slots", self.slots), ("cu_q", self.cu_q), ("ctx", self.ctx), ("last", self.last),
+        pos = self.pos if self.pos is not None else np.zeros(self.n_tok, np.int32)
+        parts = [("pos", pos), ("slots", self.slots), ("cu_q", self.cu_q), ("ctx", self.ctx), ("last", self.last),
                  ("tile_seq", self.tile_seq), ("tile_q0", self.tile_q0),
                  ("block_tables", self.block_tables.reshape(-1))]
         off = 0
@@ -120,6 +122,7 @@ def fill_meta(entries: Sequence[Entry], block_size: int, max_blocks: int, pf_til
     n_tiles = 0 if decode else sum((e.q_len + pf_tile - 1) // pf_tile for e in entries) + n_pad
 
     slots = np.empty(n_tok, np.int32)
+    posv = np.zeros(n_tok, np.int32)
     cu_q = np.zeros(n_seq + 1, np.int32)
     ctx = np.zeros(n_seq, np.int32)
     last = np.zeros(n_seq, np.int32)
@@ -135,6 +138,7 @@ def fill_meta(entries: Sequence[Entry], block_size: int, max_blocks: int, pf_til
         pos = np.arange(e.q_start, e.q_start + e.q_len)
         table = np.asarray(e.block_table, np.int64)
         slots[t:t + e.q_len] = table[pos // block_size] * block_size + pos % block_size
+        posv[t:t + e.q_len] = pos
         t += e.q_len
         cu_q[si + 1] = t
         ctx[si] = e.q_start + e.q_len
@@ -156,4 +160,4 @@ def fill_meta(entries: Sequence[Entry], block_size: int, max_blocks: int, pf_til
         ctx[si] = 0
         last[si] = t - 1
     return StepMeta(n_tok=n_tok, n_seq=n_seq, n_tiles=n_tiles, decode=decode, slots=slots, cu_q=cu_q, ctx=ctx,
-                    last=last, tile_seq=tile_seq, tile_q0=tile_q0, block_tables=bt)
+                    last=last, tile_seq=tile_seq, tile_q0=tile_q0, block_tables=bt, pos=posv)

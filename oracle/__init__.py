@@ -134,3 +134,158 @@ def ref_two_pass(q, kc, vc, block_tables, ctx_lens, cu_q, nq, nkv, hd, max_block
     if rc != 0:
         raise ValueError("oracle ref_two_pass rejected shape")
     return out
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# Non-attention ops of the CPU backend (model_oracle.c).  Arrays are uint16 (bf16 bits) or float32; the output
+# dtype is chosen by ``out_bf16`` as the reference's output tensor dtype would be.
+# ---------------------------------------------------------------------------------------------------------------
+_DT = {np.dtype(np.uint16): 1, np.dtype(np.float32): 0}
+
+
+def _t(a):
+    a = np.ascontiguousarray(a)
+    if a.dtype not in _DT:
+        raise TypeError(f"oracle ops take uint16 (bf16) or float32 arrays, got {a.dtype}")
+    return a, _DT[a.dtype]
+
+
+def _out(shape, out_bf16):
+    return np.empty(shape, np.uint16 if out_bf16 else np.float32)
+
+
+def _model_sigs(lib):
+    P, I, F = ctypes.c_void_p, ctypes.c_int64, ctypes.c_float
+    D = ctypes.c_int
+    lib.ora_embedding.argtypes = [P, P, D, P, D, I, I, I]
+    lib.ora_embedding.restype = ctypes.c_int
+    lib.ora_rmsnorm.argtypes = [P, D, P, D, P, D, I, I, F, F]
+    lib.ora_linear.argtypes = [P, D, P, D, P, D, I, I, I]
+    lib.ora_rope_table.argtypes = [P, P, I, I, ctypes.c_double]
+    lib.ora_rope.argtypes = [P, D, P, D, P, P, P, I, I, I, I]
+    lib.ora_silu.argtypes = [P, D, P, D, I]
+    lib.ora_add.argtypes = [P, D, P, D, P, D, I, I]
+    lib.ora_mul.argtypes = [P, D, P, D, P, D, I, I]
+    lib.ora_gather.argtypes = [P, P, P, I, I]
+    lib.ora_sample.argtypes = [P, D, P, P, ctypes.c_uint64, I, I]
+    lib.ora_splitmix64.argtypes = [ctypes.c_uint64]
+    lib.ora_splitmix64.restype = ctypes.c_uint64
+
+
+def _mlib():
+    lib = _load()
+    if not getattr(lib, "_model_sigs", False):
+        _model_sigs(lib)
+        lib._model_sigs = True
+    return lib
+
+
+def embedding(ids, table, out_bf16=True):
+    """cpu/embedding.zig: out[s] = table[ids[s]]. Raises on an out-of-range id."""
+    ids = _i32(ids)
+    table, tdt = _t(table)
+    vocab, hidden = table.shape
+    out = _out((ids.size, hidden), out_bf16)
+    if _mlib().ora_embedding(_p(ids), _p(table), tdt, _p(out), int(out_bf16), ids.size, vocab, hidden) != 0:
+        raise IndexError("token id out of range")
+    return out
+
+
+def rmsnorm(x, gain, eps, out_bf16=None, w_offset=0.0):
+    """cpu/norm.zig:57-89 over the last axis; output dtype defaults to the input's."""
+    x, xdt = _t(x)
+    gain, gdt = _t(gain)
+    n = x.shape[-1]
+    ob = xdt == 1 if out_bf16 is None else out_bf16
+    out = _out(x.shape, ob)
+    _mlib().ora_rmsnorm(_p(x), xdt, _p(gain), gdt, _p(out), int(ob), x.size // n, n, eps, w_offset)
+    return out
+
+
+def linear(x, w, out_bf16=None):
+    """cpu/linear.zig:7-28: x [..., in] @ w[out, in]^T, f32 accumulation in index order."""
+    x, xdt = _t(x)
+    w, wdt = _t(w)
+    out_dim, in_dim = w.shape
+    assert x.shape[-1] == in_dim
+    rows = x.size // in_dim
+    ob = xdt == 1 if out_bf16 is None else out_bf16
+    out = _out(x.shape[:-1] + (out_dim,), ob)
+    _mlib().ora_linear(_p(x), xdt, _p(w), wdt, _p(out), int(ob), rows, in_dim, out_dim)
+    return out
+
+
+def rope_table(max_seq, head_dim, theta):
+    """cpu/rope.zig:38-68: (cos, sin) f32 [max_seq, head_dim]."""
+    c = np.empty((max_seq, head_dim), np.float32)
+    s = np.empty((max_seq, head_dim), np.float32)
+    _mlib().ora_rope_table(_p(c), _p(s), max_seq, head_dim, float(theta))
+    return c, s
+
+
+def rope(x, pos, cos_t, sin_t, out_bf16=None, rope_dim=None):
+    """cpu/rope.zig:6-36: NEOX rotation of x [T, n_head, head_dim] at positions pos [T]."""
+    x, xdt = _t(x)
+    pos = _i32(pos)
+    T, nh, hd = x.shape
+    rd = hd if rope_dim is None else rope_dim
+    cos_t = np.ascontiguousarray(cos_t, np.float32)
+    sin_t = np.ascontiguousarray(sin_t, np.float32)
+    assert cos_t.shape[1] == rd and int(pos.max(initial=0)) < cos_t.shape[0]
+    ob = xdt == 1 if out_bf16 is None else out_bf16
+    out = _out(x.shape, ob)
+    _mlib().ora_rope(_p(x), xdt, _p(out), int(ob), _p(pos), _p(cos_t), _p(sin_t), T, nh, hd, rd)
+    return out
+
+
+def silu(x, out_bf16=None):
+    x, xdt = _t(x)
+    ob = xdt == 1 if out_bf16 is None else out_bf16
+    out = _out(x.shape, ob)
+    _mlib().ora_silu(_p(x), xdt, _p(out), int(ob), x.size)
+    return out
+
+
+def _binary(fn, a, b, out_bf16):
+    a, adt = _t(a)
+    b, bdt = _t(b)
+    assert a.size % b.size == 0
+    ob = adt == 1 if out_bf16 is None else out_bf16
+    out = _out(a.shape, ob)
+    fn(_p(a), adt, _p(b), bdt, _p(out), int(ob), a.size, b.size)
+    return out
+
+
+def add(a, b, out_bf16=None):
+    """cpu/arithmetic.zig add (b broadcast by index modulo its size)."""
+    return _binary(_mlib().ora_add, a, b, out_bf16)
+
+
+def mul(a, b, out_bf16=None):
+    """cpu/arithmetic.zig mul."""
+    return _binary(_mlib().ora_mul, a, b, out_bf16)
+
+
+def gather(x, last):
+    """cpu/memcpy.zig GatherLast: rows last[s] of x [T, H]."""
+    x = np.ascontiguousarray(x)
+    last = _i32(last)
+    assert int(last.max(initial=0)) < x.shape[0]
+    out = np.empty((last.size,) + x.shape[1:], x.dtype)
+    _mlib().ora_gather(_p(x), _p(out), _p(last), last.size, x[0].nbytes)
+    return out
+
+
+def sample(logits, temps=None, seed=0):
+    """cpu/sample.zig:12-40: greedy (temp <= 0; ties keep the smaller index) or Gumbel-max per row."""
+    logits, ldt = _t(logits)
+    S, V = logits.shape
+    temps = np.zeros(S, np.float32) if temps is None else np.ascontiguousarray(temps, np.float32)
+    out = np.empty(S, np.int32)
+    _mlib().ora_sample(_p(logits), ldt, _p(out), _p(temps), int(seed) & (2**64 - 1), S, V)
+    return out
+
+
+def splitmix64(x: int) -> int:
+    """cpu/sample.zig:5-10 (one SplitMix64 output for state x)."""
+    return int(_mlib().ora_splitmix64(int(x) & (2**64 - 1)))

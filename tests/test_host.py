@@ -2,12 +2,13 @@
 
 * step metadata restated from the executor (executor.zig:139-202, 609-632, 772-861; attention_v1.zig:51-57),
 * algorithmic work of the BASELINE configurations (the metric definitions),
-* libllmgen_attn.so loads and exports every symbol include/llmgen_attn.h declares,
+* libllmgen_attn.so loads and exports every symbol include/*.h declares,
 * launcher argument checks that return before any device call (stderr message, no launch),
 * operator error behaviour (AttentionNeedsBf16, NoAttentionManager, LayerNotActive).
 """
 from __future__ import annotations
 
+import glob
 import os
 import re
 import subprocess
@@ -110,10 +111,12 @@ def test_c4_mixed_shape():
 
 # ---------------------------------------------------------------- C-ABI library
 def _declared_symbols():
-    with open(os.path.join(ROOT, "include", "llmgen_attn.h")) as f:
-        text = f.read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(hip_\w+)\s*\(", text)))
+    names = set()
+    for header in sorted(glob.glob(os.path.join(ROOT, "include", "*.h"))):
+        with open(header) as f:
+            text = re.sub(r"/\*.*?\*/", "", f.read(), flags=re.S)
+        names.update(re.findall(r"\b(hip_\w+)\s*\(", text))
+    return sorted(names)
 
 
 def test_library_exports_every_declared_symbol():
