@@ -60,6 +60,18 @@ void hip_sample(int32_t *out_ids, const uint16_t *logits, const float *temps, co
                 void *scratch);
 size_t hip_sample_scratch_bytes(int max_S);
 
+/* Fused per-head q/k RMSNorm + NEOX RoPE + paged KV write.  No single reference extern: it replaces the sequence
+ * the reference graph runs before attention -- cuda_rmsnorm over q and k rows (norm/norm.zig:5, D = hd), cuda_rope
+ * over q and k (rope/rope.zig:9-18) and cuda_store_kv (attention/attention_v1.zig:10) -- the fusion the reference
+ * docs list as the next step (docs/llmgen-serving-unfused/23-switches-debug.html).  q, k, v [T, n, hd] bf16;
+ * q_out [T, nq, hd] (may alias q) receives the normed, rotated q; the normed, rotated k and the unchanged v go to
+ * k_cache / v_cache [num_blocks, nkv, block_size, hd] at slot_mapping[t] (slot < 0: not written).  Gains f32 [hd];
+ * tables [max_seq, hd] f32.  Outputs are bit-identical to hip_rmsnorm + hip_rope + hip_store_kv.  hd == 128. */
+void hip_qk_norm_rope_store_kv(uint16_t *q_out, uint16_t *k_cache, uint16_t *v_cache, const uint16_t *q,
+                               const uint16_t *k, const uint16_t *v, const float *q_norm_w, const float *k_norm_w,
+                               float eps, const float *cos_tab, const float *sin_tab, const int32_t *positions,
+                               const int32_t *slot_mapping, int T, int nq, int nkv, int hd, int block_size);
+
 #ifdef __cplusplus
 }
 #endif

@@ -59,6 +59,7 @@ SIGNATURES = {
     "hip_gather_rows": (None, [_P, _P, _P, _I, _I]),
     "hip_sample": (None, [_P, _P, _P, _P, _I, _I, _P]),
     "hip_sample_scratch_bytes": (_SZ, [_I]),
+    "hip_qk_norm_rope_store_kv": (None, [_P, _P, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P, _P, _I, _I, _I, _I, _I]),
 }
 
 _lib = None

@@ -128,15 +128,18 @@ class PagedAttentionImpl:
     """attention_v1.zig:60-120 for the HIP backend."""
 
     @staticmethod
-    def execute(device_id: int, out: AttnNode) -> None:
+    def execute(device_id: int, out: AttnNode, store_kv: bool = True) -> None:
+        """``store_kv=False`` when this step's k / v are already in the cache (written by the fused
+        hip_qk_norm_rope_store_kv); ``out.src[1:]`` are then not read."""
         if out.data.dtype not in _BF16_LIKE:
             raise AttentionNeedsBf16(f"attention needs bf16, got {out.data.dtype}")
         s = g_step
         kv = kv_of(out.layer_id)
         L = lib()
         q, k, v = out.src
-        L.hip_store_kv(_ptr(k), _ptr(v), s.slots, _ptr(kv.k), _ptr(kv.v), s.n_tok, s.n_kv_head, s.head_dim,
-                       s.block_size)
+        if store_kv:
+            L.hip_store_kv(_ptr(k), _ptr(v), s.slots, _ptr(kv.k), _ptr(kv.v), s.n_tok, s.n_kv_head, s.head_dim,
+                           s.block_size)
         if s.decode:
             L.hip_attn_decode(_ptr(out.data), _ptr(q), _ptr(kv.k), _ptr(kv.v), s.block_tables, s.ctx, s.n_seq,
                               s.n_head, s.n_kv_head, s.head_dim, s.max_blocks, s.block_size, s.attn_scale,

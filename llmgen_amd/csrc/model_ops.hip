@@ -1,5 +1,6 @@
 // model_ops.hip -- the non-attention ops of the Qwen3 forward (embedding, RMSNorm, linear, NEOX RoPE, SiLU,
-// add, mul, gather_last, sampling) for the end-to-end greedy-token check.
+// add, mul, gather_last, sampling) for the end-to-end greedy-token check, and the fused q/k norm + RoPE + KV
+// write that replaces five of them before attention.
 //
 // These kernels trade speed for reproducibility: every output is computed in the order the reference CPU
 // backend uses (src/backend/cpu/*.zig), with one IEEE rounding per f32 multiply / add / divide / sqrt and one
@@ -333,3 +334,99 @@ void hip_sample(int32_t *out_ids, const uint16_t *logits, const float *temps, co
 }
 
 }  // extern "C"
+
+// ------------------------------------------------------------------------------------------------------------
+// Fused per-head q/k RMSNorm + NEOX RoPE + paged KV write (one launch for what the unfused graph does in five:
+// rmsnorm(q), rmsnorm(k), rope(q), rope(k), store_kv).  One lane owns one 128-wide head row: the row stays in
+// registers from load to store, the sum of squares runs in index order in that lane and every value is rounded
+// exactly where the unfused ops round it, so the outputs are bit-identical to the unfused sequence.  Lanes
+// [0, T*nq) are q rows (written to q_out, which may alias q); lanes [T*nq, T*(nq+nkv)) are k rows, written into
+// the paged cache together with the v row of the same (token, KV head).  Slot < 0 skips the cache write.
+namespace {
+constexpr int QK_HD = 128;
+
+__global__ void __launch_bounds__(256) qk_norm_rope_store_kernel(
+    bf16_t *q_out, bf16_t *k_cache, bf16_t *v_cache, const bf16_t *q, const bf16_t *k, const bf16_t *v,
+    const float *q_w, const float *k_w, float eps, const float *cos_t, const float *sin_t, const int *pos,
+    const int *slots, int T, int nq, int nkv, int block_size) {
+    const long r = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long rows_q = (long)T * nq;
+    if (r >= rows_q + (long)T * nkv) return;
+    const bool is_q = r < rows_q;
+    const long rk = r - rows_q;
+    const int t = is_q ? (int)(r / nq) : (int)(rk / nkv);
+    const int h = is_q ? 0 : (int)(rk % nkv);
+    const bf16_t *src = is_q ? q + r * QK_HD : k + rk * QK_HD;
+    const float *w = is_q ? q_w : k_w;
+
+    u32x4_t xv[16];
+#pragma unroll
+    for (int c = 0; c < 16; ++c) xv[c] = ld16(src + c * 8);
+    float ss = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 16; ++c)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float lo = bf16lo_to_f32(xv[c][e]), hi = bf16hi_to_f32(xv[c][e]);
+            ss += lo * lo;
+            ss += hi * hi;
+        }
+    const float scale = 1.0f / sqrtf(ss / (float)QK_HD + eps);
+    // normed (bf16) values, two per dword, in place
+#pragma unroll
+    for (int c = 0; c < 16; ++c)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int i = c * 8 + 2 * e;
+            const float n0 = (float)(__bf16)(bf16lo_to_f32(xv[c][e]) * scale);
+            const float n1 = (float)(__bf16)(bf16hi_to_f32(xv[c][e]) * scale);
+            xv[c][e] = pack_bf16x2(n0 * w[i], n1 * w[i + 1]);
+        }
+    // rope: pairs (i, i + 64) sit in dword vectors c and c + 8
+    const float *cr = cos_t + (long)pos[t] * QK_HD;
+    const float *sr = sin_t + (long)pos[t] * QK_HD;
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int i = c * 8 + 2 * e;
+            const float a0 = bf16lo_to_f32(xv[c][e]), a1 = bf16hi_to_f32(xv[c][e]);
+            const float b0 = bf16lo_to_f32(xv[c + 8][e]), b1 = bf16hi_to_f32(xv[c + 8][e]);
+            const float c0 = cr[i], c1 = cr[i + 1], s0 = sr[i], s1 = sr[i + 1];
+            xv[c][e] = pack_bf16x2(a0 * c0 - b0 * s0, a1 * c1 - b1 * s1);
+            xv[c + 8][e] = pack_bf16x2(b0 * c0 + a0 * s0, b1 * c1 + a1 * s1);
+        }
+    if (is_q) {
+        bf16_t *dst = q_out + r * QK_HD;
+#pragma unroll
+        for (int c = 0; c < 16; ++c) *reinterpret_cast<u32x4_t *>(dst + c * 8) = xv[c];
+        return;
+    }
+    const int slot = slots[t];
+    if (slot < 0) return;
+    const long off = (((long)(slot / block_size) * nkv + h) * block_size + slot % block_size) * QK_HD;
+    const bf16_t *vsrc = v + rk * QK_HD;
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+        *reinterpret_cast<u32x4_t *>(k_cache + off + c * 8) = xv[c];
+        *reinterpret_cast<u32x4_t *>(v_cache + off + c * 8) = ld16(vsrc + c * 8);
+    }
+}
+}  // namespace
+
+extern "C" void hip_qk_norm_rope_store_kv(uint16_t *q_out, uint16_t *k_cache, uint16_t *v_cache, const uint16_t *q,
+                                          const uint16_t *k, const uint16_t *v, const float *q_norm_w,
+                                          const float *k_norm_w, float eps, const float *cos_tab,
+                                          const float *sin_tab, const int32_t *positions,
+                                          const int32_t *slot_mapping, int T, int nq, int nkv, int hd,
+                                          int block_size) {
+    if (T <= 0) return;
+    if (hd != QK_HD || nq <= 0 || nkv <= 0 || block_size <= 0) {
+        reject("hip_qk_norm_rope_store_kv: needs hd == 128 and positive nq, nkv, block_size");
+        return;
+    }
+    const size_t rows = (size_t)T * (nq + nkv);
+    qk_norm_rope_store_kernel<<<blocks_for(rows, 256), 256, 0, g_llmgen_stream>>>(
+        q_out, k_cache, v_cache, q, k, v, q_norm_w, k_norm_w, eps, cos_tab, sin_tab, positions, slot_mapping, T, nq,
+        nkv, block_size);
+}

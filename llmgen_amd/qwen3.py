@@ -139,7 +139,10 @@ class Qwen3:
     def _empty(self, *shape, dtype=torch.int16):
         return torch.empty(shape, dtype=dtype, device=self.device)
 
-    def forward(self, entries: Sequence[stepmod.Entry], ids: Sequence[int], temps=None, seed: int = 0) -> List[int]:
+    def forward(self, entries: Sequence[stepmod.Entry], ids: Sequence[int], temps=None, seed: int = 0,
+                fused_qk: bool = True) -> List[int]:
+        """``fused_qk`` runs q/k norm + RoPE + the KV write as one kernel (hip_qk_norm_rope_store_kv); the unfused
+        path runs the reference graph's five launches.  Both give identical values."""
         cfg, L = self.cfg, self.L
         meta = stepmod.fill_meta(entries, cfg.block_size, self.max_blocks, self.pf_tile)
         T, S = meta.n_tok, meta.n_seq
@@ -172,11 +175,18 @@ class Qwen3:
             L.hip_linear(p(q), 0, p(xn), p(W[b + "attn_q.weight"]), T, nq * hd, H)
             L.hip_linear(p(k), 0, p(xn), p(W[b + "attn_k.weight"]), T, nkv * hd, H)
             L.hip_linear(p(v), 0, p(xn), p(W[b + "attn_v.weight"]), T, nkv * hd, H)
-            L.hip_rmsnorm(p(q), p(q), p(W[b + "attn_q_norm.weight"]), T * nq, hd, cfg.rms_eps)
-            L.hip_rmsnorm(p(k), p(k), p(W[b + "attn_k_norm.weight"]), T * nkv, hd, cfg.rms_eps)
-            L.hip_rope(p(q), p(q), p(self.cos), p(self.sin), g.pos, T, nq, hd)
-            L.hip_rope(p(k), p(k), p(self.cos), p(self.sin), g.pos, T, nkv, hd)
-            A.PagedAttentionImpl.execute(0, A.AttnNode(data=attn, src=[q, k, v], layer_id=i))
+            if fused_qk:
+                kv = A.kv_of(i)
+                L.hip_qk_norm_rope_store_kv(p(q), p(kv.k), p(kv.v), p(q), p(k), p(v),
+                                            p(W[b + "attn_q_norm.weight"]), p(W[b + "attn_k_norm.weight"]),
+                                            cfg.rms_eps, p(self.cos), p(self.sin), g.pos, g.slots, T, nq, nkv, hd,
+                                            cfg.block_size)
+            else:
+                L.hip_rmsnorm(p(q), p(q), p(W[b + "attn_q_norm.weight"]), T * nq, hd, cfg.rms_eps)
+                L.hip_rmsnorm(p(k), p(k), p(W[b + "attn_k_norm.weight"]), T * nkv, hd, cfg.rms_eps)
+                L.hip_rope(p(q), p(q), p(self.cos), p(self.sin), g.pos, T, nq, hd)
+                L.hip_rope(p(k), p(k), p(self.cos), p(self.sin), g.pos, T, nkv, hd)
+            A.PagedAttentionImpl.execute(0, A.AttnNode(data=attn, src=[q, k, v], layer_id=i), store_kv=not fused_qk)
             L.hip_linear(p(o), 0, p(attn), p(W[b + "attn_output.weight"]), T, H, nq * hd)
             L.hip_add(p(x), p(x), p(o), T * H)
             L.hip_rmsnorm(p(xn), p(x), p(W[b + "ffn_norm.weight"]), T, H, cfg.rms_eps)

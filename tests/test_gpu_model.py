@@ -186,7 +186,7 @@ def test_qwen3_greedy_ids_match_cpu_backend(qwen_pair):
     for step in range(7):
         meta = S.fill_meta(ents, cfg.block_size, mb, G.pf_tile)
         print(f"[qwen3] step {step} n_tok {meta.n_tok} decode {meta.decode}", flush=True)
-        ids_g = G.forward(ents, ids_in)
+        ids_g = G.forward(ents, ids_in, fused_qk=(step % 2 == 0))  # both pre-attention paths
         ids_c, lg_c = C.forward(meta, ids_in, mb, return_logits=True)
         _, lg_c2 = C2.forward(meta, ids_in, mb, return_logits=True)
         errs.append(_logit_err(down(G.last_logits), lg_c))
@@ -203,3 +203,52 @@ def test_qwen3_greedy_ids_match_cpu_backend(qwen_pair):
     check_err()
     for e, f in zip(errs, floors):
         assert e[1] <= 2 * f[1] + 1e-3, (errs, floors)
+
+
+@pytest.mark.parametrize("T,nq,nkv,bs,nb", [(32, 16, 8, 256, 40), (300, 32, 8, 16, 64), (5, 16, 16, 16, 8)])
+def test_fused_qk_norm_rope_store_kv_matches_unfused(gpu, T, nq, nkv, bs, nb):
+    from llmgen_amd.qwen3 import rope_tables
+
+    rng = np.random.default_rng(T + nq)
+    hd = 128
+    q, k, v = rbf16(rng, (T, nq, hd), 2.0), rbf16(rng, (T, nkv, hd), 2.0), rbf16(rng, (T, nkv, hd))
+    qw = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    kw = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    pos = rng.integers(0, 1024, T).astype(np.int32)
+    slots = rng.permutation(nb * bs)[:T].astype(np.int32)
+    slots[::7] = -1  # rows that must not be written
+    c, s = rope_tables(1024, hd, 1e6)
+    L = lib()
+    d = {name: up(a) for name, a in dict(q=q, k=k, v=v, qw=qw, kw=kw, pos=pos, slots=slots, c=c, s=s).items()}
+    shape = (nb, nkv, bs, hd)
+    kc_f, vc_f = (torch.zeros(shape, dtype=torch.int16, device=gpu) for _ in range(2))
+    kc_u, vc_u = (torch.zeros(shape, dtype=torch.int16, device=gpu) for _ in range(2))
+    q_f = torch.empty_like(d["q"])
+    P = lambda t: t.data_ptr()  # noqa: E731
+    L.hip_qk_norm_rope_store_kv(P(q_f), P(kc_f), P(vc_f), P(d["q"]), P(d["k"]), P(d["v"]), P(d["qw"]), P(d["kw"]),
+                                1e-6, P(d["c"]), P(d["s"]), P(d["pos"]), P(d["slots"]), T, nq, nkv, hd, bs)
+    # unfused: the reference graph's five launches
+    q_u, k_u = d["q"].clone(), d["k"].clone()
+    L.hip_rmsnorm(P(q_u), P(q_u), P(d["qw"]), T * nq, hd, 1e-6)
+    L.hip_rmsnorm(P(k_u), P(k_u), P(d["kw"]), T * nkv, hd, 1e-6)
+    L.hip_rope(P(q_u), P(q_u), P(d["c"]), P(d["s"]), P(d["pos"]), T, nq, hd)
+    L.hip_rope(P(k_u), P(k_u), P(d["c"]), P(d["s"]), P(d["pos"]), T, nkv, hd)
+    L.hip_store_kv(P(k_u), P(d["v"]), P(d["slots"]), P(kc_u), P(vc_u), T, nkv, hd, bs)
+    # in-place variant (q_out aliases q)
+    q_i = d["q"].clone()
+    kc_i, vc_i = torch.zeros_like(kc_f), torch.zeros_like(vc_f)
+    L.hip_qk_norm_rope_store_kv(P(q_i), P(kc_i), P(vc_i), P(q_i), P(d["k"]), P(d["v"]), P(d["qw"]), P(d["kw"]),
+                                1e-6, P(d["c"]), P(d["s"]), P(d["pos"]), P(d["slots"]), T, nq, nkv, hd, bs)
+    check_err()
+    np.testing.assert_array_equal(down(q_f), down(q_u))
+    np.testing.assert_array_equal(down(q_i), down(q_u))
+    for a, b in ((kc_f, kc_u), (vc_f, vc_u), (kc_i, kc_u), (vc_i, vc_u)):
+        np.testing.assert_array_equal(down(a), down(b))
+    # and against the oracle's restated CPU ops
+    qo = O.rope(O.rmsnorm(q, qw, 1e-6), pos, c, s)
+    np.testing.assert_array_equal(down(q_f), qo)
+    ko = O.rope(O.rmsnorm(k, kw, 1e-6), pos, c, s)
+    kc_o, vc_o = np.zeros(shape, np.uint16), np.zeros(shape, np.uint16)
+    O.store_kv(ko, v, slots, kc_o, vc_o, nkv, hd, bs)
+    np.testing.assert_array_equal(down(kc_f), kc_o)
+    np.testing.assert_array_equal(down(vc_f), vc_o)
