@@ -129,6 +129,44 @@ def bench_extra(name: str, iters: int) -> dict:
     return r
 
 
+def bench_qk_fused(name: str, iters: int) -> dict:
+    """The pre-attention step of one layer for a config's token shape: q/k RMSNorm + RoPE + KV write as one
+    fused launch (hip_qk_norm_rope_store_kv) against the unfused graph's five launches (2 x rmsnorm, 2 x rope,
+    store_kv).  Bytes = q, k, v read + q, K, V written (2 * T * (nq + 2 nkv) * hd * 2 B)."""
+    import torch
+    from llmgen_amd.qwen3 import rope_tables
+
+    st = Step(name)
+    wl, g, L = st.wl, st.g, st.L
+    T = g.n_tok
+    P = lambda t: t.data_ptr()  # noqa: E731
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    qw = 1 + 0.1 * torch.randn(wl.hd, device="cuda", generator=gen)
+    kw = 1 + 0.1 * torch.randn(wl.hd, device="cuda", generator=gen)
+    c, s = (torch.from_numpy(a).cuda() for a in rope_tables(wl.max_model_len, wl.hd, 1e6))
+    pos = torch.from_numpy(st.meta.pos).cuda()
+    q, k, v = st.t["q"], st.t["k"], st.t["v"]
+    qo, k2 = torch.empty_like(q), torch.empty_like(k)
+    kc, vc = st.layer.k, st.layer.v
+
+    def fused():
+        L.hip_qk_norm_rope_store_kv(P(qo), P(kc), P(vc), P(q), P(k), P(v), P(qw), P(kw), 1e-6, P(c), P(s), P(pos),
+                                    g.slots, T, wl.nq, wl.nkv, wl.hd, wl.block_size)
+
+    def unfused():
+        L.hip_rmsnorm(P(qo), P(q), P(qw), T * wl.nq, wl.hd, 1e-6)
+        L.hip_rmsnorm(P(k2), P(k), P(kw), T * wl.nkv, wl.hd, 1e-6)
+        L.hip_rope(P(qo), P(qo), P(c), P(s), P(pos), T, wl.nq, wl.hd)
+        L.hip_rope(P(k2), P(k2), P(c), P(s), P(pos), T, wl.nkv, wl.hd)
+        L.hip_store_kv(P(k2), P(v), g.slots, P(kc), P(vc), T, wl.nkv, wl.hd, wl.block_size)
+
+    ms_f = time_launches(fused, iters, warmup=2)
+    ms_u = time_launches(unfused, iters, warmup=2)
+    nbytes = 2 * T * (wl.nq + 2 * wl.nkv) * wl.hd * 2
+    return {"config": name, "tokens": T, "fused_us": round(ms_f * 1e3, 2), "unfused_us": round(ms_u * 1e3, 2),
+            "speedup": round(ms_u / ms_f, 2), "fused_GBs": round(nbytes / (ms_f * 1e-3) / 1e9, 1)}
+
+
 def cpu_baseline(st: "Step", budget_s: float = 10.0) -> dict:
     """The CPU oracle (single thread, like the reference's scalar loop) on full c2 steps, repeated until
     ``budget_s`` seconds of CPU work; value in the metric's unit (GB/s of algorithmic decode bytes)."""
@@ -203,6 +241,9 @@ def main() -> int:
         print(json.dumps({"copy_bytes": n, "launches": args.steps}), flush=True)
         return 0
 
+    if args.only and args.only.startswith("qk_fused_"):
+        print(json.dumps(bench_qk_fused(args.only[len("qk_fused_"):], args.steps)), flush=True)
+        return 0
     if args.only:
         st = Step(args.only)
         ms = time_launches(st.attn, args.steps, args.warmup)
@@ -252,6 +293,12 @@ def main() -> int:
                 extra[name] = bench_extra(name, iters=20 if name != "c5p" else 5)
             except Exception as e:  # report, keep the headline line
                 extra[name] = {"error": repr(e)}
+            torch.cuda.empty_cache()
+        for name in ("c2", "c5p"):
+            try:
+                extra["qk_fused_" + name] = bench_qk_fused(name, iters=20)
+            except Exception as e:
+                extra["qk_fused_" + name] = {"error": repr(e)}
             torch.cuda.empty_cache()
 
     line = {

@@ -337,80 +337,92 @@ void hip_sample(int32_t *out_ids, const uint16_t *logits, const float *temps, co
 
 // ------------------------------------------------------------------------------------------------------------
 // Fused per-head q/k RMSNorm + NEOX RoPE + paged KV write (one launch for what the unfused graph does in five:
-// rmsnorm(q), rmsnorm(k), rope(q), rope(k), store_kv).  One lane owns one 128-wide head row: the row stays in
-// registers from load to store, the sum of squares runs in index order in that lane and every value is rounded
-// exactly where the unfused ops round it, so the outputs are bit-identical to the unfused sequence.  Lanes
-// [0, T*nq) are q rows (written to q_out, which may alias q); lanes [T*nq, T*(nq+nkv)) are k rows, written into
+// rmsnorm(q), rmsnorm(k), rope(q), rope(k), store_kv).  Eight lanes own one 128-wide head row, 16 elements each
+// (two 16-byte loads, coalesced), and the row stays in registers from load to store.  Every value is rounded
+// exactly where the unfused ops round it, and the sum of squares is formed in index order: lane j of the row
+// continues the running sum it receives from lane j-1 (a DPP shift per step, eight steps), so the outputs are
+// bit-identical to the unfused sequence.  RoPE partners (i, i + 64) sit in lanes j and j ^ 4.  Rows
+// [0, T*nq) are q rows (written to q_out, which may alias q); rows [T*nq, T*(nq+nkv)) are k rows, written into
 // the paged cache together with the v row of the same (token, KV head).  Slot < 0 skips the cache write.
 namespace {
 constexpr int QK_HD = 128;
+constexpr int QK_LPR = 8;  // lanes per row
 
 __global__ void __launch_bounds__(256) qk_norm_rope_store_kernel(
     bf16_t *q_out, bf16_t *k_cache, bf16_t *v_cache, const bf16_t *q, const bf16_t *k, const bf16_t *v,
     const float *q_w, const float *k_w, float eps, const float *cos_t, const float *sin_t, const int *pos,
     const int *slots, int T, int nq, int nkv, int block_size) {
-    const long r = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    const long rows_q = (long)T * nq;
-    if (r >= rows_q + (long)T * nkv) return;
+    const long gt = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    const int sub = threadIdx.x & (QK_LPR - 1);
+    const long rows_q = (long)T * nq, rows = rows_q + (long)T * nkv;
+    const bool valid = gt / QK_LPR < rows;
+    const long r = valid ? gt / QK_LPR : rows - 1;  // out-of-range lanes still take part in the exchanges
     const bool is_q = r < rows_q;
     const long rk = r - rows_q;
     const int t = is_q ? (int)(r / nq) : (int)(rk / nkv);
     const int h = is_q ? 0 : (int)(rk % nkv);
-    const bf16_t *src = is_q ? q + r * QK_HD : k + rk * QK_HD;
-    const float *w = is_q ? q_w : k_w;
+    const bf16_t *src = (is_q ? q + r * QK_HD : k + rk * QK_HD) + sub * 16;
+    const float *w = (is_q ? q_w : k_w) + sub * 16;
 
-    u32x4_t xv[16];
+    u32x4_t xv[2] = {ld16(src), ld16(src + 8)};
+    float x[16];
+    unpack_bf16x8(xv[0], x);
+    unpack_bf16x8(xv[1], x + 8);
+    // running sum of squares in index order across the row's eight lanes
+    float in = 0.0f, cand = 0.0f;
 #pragma unroll
-    for (int c = 0; c < 16; ++c) xv[c] = ld16(src + c * 8);
-    float ss = 0.0f;
+    for (int step = 0; step < QK_LPR; ++step) {
+        cand = in;
 #pragma unroll
-    for (int c = 0; c < 16; ++c)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float lo = bf16lo_to_f32(xv[c][e]), hi = bf16hi_to_f32(xv[c][e]);
-            ss += lo * lo;
-            ss += hi * hi;
-        }
+        for (int e = 0; e < 16; ++e) cand += x[e] * x[e];
+        // row_shr:1 -- lane j receives lane j-1's running sum (lane 0 of each row starts from 0)
+        const float prev = __builtin_bit_cast(
+            float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, cand), 0x111, 0xF, 0xF, false));
+        in = sub ? prev : 0.0f;
+    }
+    // the last lane of the row holds the complete sum
+    const int last_lane = (__lane_id() & ~(QK_LPR - 1)) | (QK_LPR - 1);
+    const float ss = __builtin_bit_cast(
+        float, __builtin_amdgcn_ds_bpermute(last_lane << 2, __builtin_bit_cast(int, cand)));
     const float scale = 1.0f / sqrtf(ss / (float)QK_HD + eps);
-    // normed (bf16) values, two per dword, in place
+    float n[16];
 #pragma unroll
-    for (int c = 0; c < 16; ++c)
+    for (int e = 0; e < 16; ++e) n[e] = bf2f(f2bf(bf2f(f2bf(x[e] * scale)) * w[e]));
+    // RoPE: lanes 0-3 hold dims i < 64 (x0), lanes 4-7 their partners i + 64 (x1); cos/sin rows repeat per half
+    float other[16];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int i = c * 8 + 2 * e;
-            const float n0 = (float)(__bf16)(bf16lo_to_f32(xv[c][e]) * scale);
-            const float n1 = (float)(__bf16)(bf16hi_to_f32(xv[c][e]) * scale);
-            xv[c][e] = pack_bf16x2(n0 * w[i], n1 * w[i + 1]);
+    for (int e = 0; e < 16; ++e) other[e] = lane_xor(n[e], 4);
+    const int dim0 = sub * 16;
+    const float *cr = cos_t + (long)pos[t] * QK_HD + dim0;
+    const float *sr = sin_t + (long)pos[t] * QK_HD + dim0;
+    const bool low = sub < 4;
+    u32x4_t ov[2];
+#pragma unroll
+    for (int e = 0; e < 16; e += 2) {
+        float o2[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const float c = cr[e + u], s = sr[e + u];
+            o2[u] = low ? n[e + u] * c - other[e + u] * s : n[e + u] * c + other[e + u] * s;
         }
-    // rope: pairs (i, i + 64) sit in dword vectors c and c + 8
-    const float *cr = cos_t + (long)pos[t] * QK_HD;
-    const float *sr = sin_t + (long)pos[t] * QK_HD;
-#pragma unroll
-    for (int c = 0; c < 8; ++c)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int i = c * 8 + 2 * e;
-            const float a0 = bf16lo_to_f32(xv[c][e]), a1 = bf16hi_to_f32(xv[c][e]);
-            const float b0 = bf16lo_to_f32(xv[c + 8][e]), b1 = bf16hi_to_f32(xv[c + 8][e]);
-            const float c0 = cr[i], c1 = cr[i + 1], s0 = sr[i], s1 = sr[i + 1];
-            xv[c][e] = pack_bf16x2(a0 * c0 - b0 * s0, a1 * c1 - b1 * s1);
-            xv[c + 8][e] = pack_bf16x2(b0 * c0 + a0 * s0, b1 * c1 + a1 * s1);
-        }
+        ov[e >> 3][(e & 7) >> 1] = pack_bf16x2(o2[0], o2[1]);
+    }
+    if (!valid) return;
     if (is_q) {
-        bf16_t *dst = q_out + r * QK_HD;
-#pragma unroll
-        for (int c = 0; c < 16; ++c) *reinterpret_cast<u32x4_t *>(dst + c * 8) = xv[c];
+        bf16_t *dst = q_out + r * QK_HD + dim0;
+        *reinterpret_cast<u32x4_t *>(dst) = ov[0];
+        *reinterpret_cast<u32x4_t *>(dst + 8) = ov[1];
         return;
     }
     const int slot = slots[t];
     if (slot < 0) return;
-    const long off = (((long)(slot / block_size) * nkv + h) * block_size + slot % block_size) * QK_HD;
-    const bf16_t *vsrc = v + rk * QK_HD;
-#pragma unroll
-    for (int c = 0; c < 16; ++c) {
-        *reinterpret_cast<u32x4_t *>(k_cache + off + c * 8) = xv[c];
-        *reinterpret_cast<u32x4_t *>(v_cache + off + c * 8) = ld16(vsrc + c * 8);
-    }
+    const long off = (((long)(slot / block_size) * nkv + h) * block_size + slot % block_size) * QK_HD + dim0;
+    const bf16_t *vsrc = v + rk * QK_HD + dim0;
+    const u32x4_t v0 = ld16(vsrc), v1 = ld16(vsrc + 8);
+    *reinterpret_cast<u32x4_t *>(k_cache + off) = ov[0];
+    *reinterpret_cast<u32x4_t *>(k_cache + off + 8) = ov[1];
+    *reinterpret_cast<u32x4_t *>(v_cache + off) = v0;
+    *reinterpret_cast<u32x4_t *>(v_cache + off + 8) = v1;
 }
 }  // namespace
 
@@ -425,8 +437,8 @@ extern "C" void hip_qk_norm_rope_store_kv(uint16_t *q_out, uint16_t *k_cache, ui
         reject("hip_qk_norm_rope_store_kv: needs hd == 128 and positive nq, nkv, block_size");
         return;
     }
-    const size_t rows = (size_t)T * (nq + nkv);
-    qk_norm_rope_store_kernel<<<blocks_for(rows, 256), 256, 0, g_llmgen_stream>>>(
+    const size_t threads = (size_t)T * (nq + nkv) * QK_LPR;
+    qk_norm_rope_store_kernel<<<blocks_for(threads, 256), 256, 0, g_llmgen_stream>>>(
         q_out, k_cache, v_cache, q, k, v, q_norm_w, k_norm_w, eps, cos_tab, sin_tab, positions, slot_mapping, T, nq,
         nkv, block_size);
 }
