@@ -50,6 +50,17 @@ void hip_attn_decode(uint16_t *out, const uint16_t *q, const uint16_t *k_cache, 
                      int max_blocks, int block_size, float scale, float *part_o, float *part_ml, int part_size,
                      int max_parts);
 
+/* No single reference extern: the pair cuda_store_kv + cuda_attn_decode that PagedAttentionImpl issues for a decode
+ * step (attention_v1.zig:65-95), fused into one launch.  k, v [S, nkv, hd] hold the step's one token per sequence,
+ * slot_mapping[s] its cache slot, which must be the slot of position ctx_lens[s] - 1 under block_tables[s] (as
+ * the engine's metadata guarantees).  The cache receives exactly what hip_store_kv would write (slot < 0: nothing)
+ * and out equals hip_store_kv followed by hip_attn_decode.  Other arguments as hip_attn_decode. */
+void hip_attn_decode_store_kv(uint16_t *out, const uint16_t *q, const uint16_t *k, const uint16_t *v,
+                              const int32_t *slot_mapping, uint16_t *k_cache, uint16_t *v_cache,
+                              const int32_t *block_tables, const int32_t *ctx_lens, int S, int nq, int nkv, int hd,
+                              int max_blocks, int block_size, float scale, float *part_o, float *part_ml,
+                              int part_size, int max_parts);
+
 /* Replaces cuda_attn_prefill (attention_v1.zig:30-47).  Causal varlen attention over the paged cache: sequence
  * s owns rows [cu_q[s], cu_q[s+1]) of q / out [T, nq, hd]; ctx_lens[s] = keys after this step; row j sits at
  * position ctx - q_len + j and attends to keys 0..pos.  Sequences with ctx < q_len are padding: rows of 0.

@@ -125,7 +125,8 @@ def _ptr(t: torch.Tensor) -> int:
 
 
 class PagedAttentionImpl:
-    """attention_v1.zig:60-120 for the HIP backend."""
+    """attention_v1.zig:60-120 for the HIP backend.  Decode steps issue store_kv and split-K decode as one fused
+    launch (hip_attn_decode_store_kv); prefill / mixed steps issue store_kv, then prefill, as the reference does."""
 
     @staticmethod
     def execute(device_id: int, out: AttnNode, store_kv: bool = True) -> None:
@@ -137,6 +138,13 @@ class PagedAttentionImpl:
         kv = kv_of(out.layer_id)
         L = lib()
         q, k, v = out.src
+        if s.decode and store_kv:
+            # store_kv fused into the decode launch (one kernel per decode step)
+            L.hip_attn_decode_store_kv(_ptr(out.data), _ptr(q), _ptr(k), _ptr(v), s.slots, _ptr(kv.k), _ptr(kv.v),
+                                       s.block_tables, s.ctx, s.n_seq, s.n_head, s.n_kv_head, s.head_dim,
+                                       s.max_blocks, s.block_size, s.attn_scale, s.part_o, s.part_ml,
+                                       stepmod.part_size(s.n_seq), stepmod.max_parts(s.n_seq, s.max_model_len))
+            return
         if store_kv:
             L.hip_store_kv(_ptr(k), _ptr(v), s.slots, _ptr(kv.k), _ptr(kv.v), s.n_tok, s.n_kv_head, s.head_dim,
                            s.block_size)

@@ -17,9 +17,13 @@
 //     per-wave LDS buffer to the PV lanes, which hold 8 head dims of 4 tokens per 16-byte V vector and
 //     accumulate all G heads in fp32 registers;
 //   * the four waves merge (max, sum, unnormalised o) through LDS; a part that is the only part of its
-//     sequence writes the final bf16 row directly, otherwise (o, m, l) go to the caller's scratch and
-//     attn_decode_reduce merges the parts with the log-sum-exp rule (attention.cu:186-207).
-// Grid = (nkv, S, max_parts) from host integers only, so the launch is graph-capturable; parts past ctx exit.
+//     sequence writes the final bf16 row directly, otherwise (o, m, l) go to the caller's scratch and the last
+//     workgroup of the (sequence, kv head) to finish merges the parts with the log-sum-exp rule
+//     (attention.cu:186-207), elected by a self-resetting counter (attn_decode_reduce_kernel when the launch
+//     has more pairs than counters);
+//   * hip_attn_decode_store_kv also writes the step's token into the cache (the store_kv of a decode step),
+//     reading that token's K/V from the step's k / v rather than from the slot being written.
+// Grid = (nkv, S, parts) from host integers only, so the launch is graph-capturable; parts past ctx exit.
 #include "hip_common.h"
 
 #include <math.h>
@@ -41,7 +45,7 @@ __device__ __forceinline__ int blk_index(int t, int block_size, int bs_shift) {
 // tokens).  Each workgroup streams `span` tokens of one (kv head, sequence) pair: round r+1's block-table and
 // K/V loads are issued before round r is computed (register double buffering), so every wave keeps one round
 // of loads in flight while it computes.
-template <int G, int NT, bool POW2, bool PIPE>
+template <int G, int NT, bool POW2, bool PIPE, bool FUSE>
 __global__ void __launch_bounds__(DEC_THREADS) __attribute__((amdgpu_waves_per_eu(G >= 16 ? 1 : (PIPE || G >= 8 ? 2 : (G >= 4 ? 3 : 4)))))
     attn_decode_split_kernel(bf16_t *__restrict__ out, float *__restrict__ part_o, float *__restrict__ part_ml,
                              const bf16_t *__restrict__ q, const bf16_t *__restrict__ kc,
@@ -49,7 +53,9 @@ __global__ void __launch_bounds__(DEC_THREADS) __attribute__((amdgpu_waves_per_e
                              const int *__restrict__ ctx_lens, int nq, int nkv, int max_blocks, int block_size,
                              int bs_shift, float scale_log2, int span, int max_parts, int nparts,
                              int *__restrict__ counters, const int *__restrict__ cu_q,
-                             const int *__restrict__ tile_seq) {
+                             const int *__restrict__ tile_seq, const bf16_t *__restrict__ k_new,
+                             const bf16_t *__restrict__ v_new, const int *__restrict__ slots,
+                             bf16_t *__restrict__ kc_w, bf16_t *__restrict__ vc_w) {
     constexpr int WTOK = NT * 16;              // tokens per wave per round
     constexpr int RTOK = DEC_WAVES * WTOK;     // tokens per round
     const int kvh = blockIdx.x, part = blockIdx.z;
@@ -63,6 +69,22 @@ __global__ void __launch_bounds__(DEC_THREADS) __attribute__((amdgpu_waves_per_e
     }
     const int ctx = ctx_lens[s];
     const int t0 = part * span;
+    // Fused KV write (decode launch only): this step's token sits at position ctx - 1.  Part 0 copies its K/V
+    // rows into the cache slot; the workgroup whose span holds position ctx - 1 reads them from k_new / v_new,
+    // so no workgroup of this launch reads the slot being written.
+    constexpr bool fuse = FUSE;
+    const long new_row = ((long)row * nkv + kvh) * HD;
+    if (fuse && part == 0 && ctx > 0 && threadIdx.x < 32) {
+        const int slot = slots[row];
+        if (slot >= 0) {
+            const long dst = (((long)(slot / block_size) * nkv + kvh) * block_size + slot % block_size) * HD;
+            const int c = threadIdx.x & 15;
+            if (threadIdx.x < 16)
+                *reinterpret_cast<u32x4_t *>(kc_w + dst + c * 8) = ld16(k_new + new_row + c * 8);
+            else
+                *reinterpret_cast<u32x4_t *>(vc_w + dst + c * 8) = ld16(v_new + new_row + c * 8);
+        }
+    }
     if (t0 >= ctx) {
         if (ctx <= 0 && part == 0) {  // padding row: zeros (cpu/attention.zig:80-83)
             for (int idx = threadIdx.x; idx < G * HD; idx += DEC_THREADS)
@@ -144,13 +166,16 @@ __global__ void __launch_bounds__(DEC_THREADS) __attribute__((amdgpu_waves_per_e
         for (int tau = 0; tau < NT; ++tau) {
             const int off = kt[tau] - blk_index<POW2>(kt[tau], block_size, bs_shift) * block_size;
             const bf16_t *kr = kbase + (long)kblk[tau] * blk_stride + (long)off * HD + rgrp * 8;
+            if (fuse && kt[tau] == ctx - 1) kr = k_new + new_row + rgrp * 8;
 #pragma unroll
             for (int c = 0; c < 4; ++c) b.kf[tau][c] = ld16(kr + c * 32);
         }
 #pragma unroll
         for (int j = 0; j < 4 * NT; ++j) {
             const int off = vt[j] - blk_index<POW2>(vt[j], block_size, bs_shift) * block_size;
-            b.vf[j] = ld16(vbase + (long)vblk[j] * blk_stride + (long)off * HD + col * 8);
+            const bf16_t *vr = vbase + (long)vblk[j] * blk_stride + (long)off * HD + col * 8;
+            if (fuse && vt[j] == ctx - 1) vr = v_new + new_row + col * 8;
+            b.vf[j] = ld16(vr);
         }
     };
 
@@ -392,14 +417,20 @@ struct DecodeArgs {
     int *counters;  // merge counters (nullptr: the separate merge kernel runs)
     const int *cu_q = nullptr, *tile_seq = nullptr;  // prefill-metadata launch (single-row segments)
     hipStream_t stream = nullptr;                    // nullptr: the library's launch stream
+    const bf16_t *k_new = nullptr, *v_new = nullptr;  // fused KV write of this step's token (decode launch)
+    const int *slots = nullptr;
+    bf16_t *kc_w = nullptr, *vc_w = nullptr;
 };
 
 template <int G, int NT, bool POW2, bool PIPE>
 void launch_split(dim3 grid, const DecodeArgs &a) {
-    hipLaunchKernelGGL((attn_decode_split_kernel<G, NT, POW2, PIPE>), grid, dim3(DEC_THREADS), 0,
+    auto kern = a.k_new ? attn_decode_split_kernel<G, NT, POW2, PIPE, true>
+                        : attn_decode_split_kernel<G, NT, POW2, PIPE, false>;
+    hipLaunchKernelGGL(kern, grid, dim3(DEC_THREADS), 0,
                        a.stream ? a.stream : g_llmgen_stream, a.out,
                        a.part_o, a.part_ml, a.q, a.kc, a.vc, a.bt, a.ctx, a.nq, a.nkv, a.max_blocks, a.block_size,
-                       a.bs_shift, a.sl2, a.span, a.max_parts, a.nparts, a.counters, a.cu_q, a.tile_seq);
+                       a.bs_shift, a.sl2, a.span, a.max_parts, a.nparts, a.counters, a.cu_q, a.tile_seq, a.k_new,
+                       a.v_new, a.slots, a.kc_w, a.vc_w);
 }
 
 template <int G, int NT>
@@ -465,12 +496,11 @@ void launch_decode_rows(dim3 grid, const DecodeArgs &a, int G) {
     }
 }
 
-}  // namespace
 
-extern "C" void hip_attn_decode(bf16_t *out, const bf16_t *q, const bf16_t *k_cache, const bf16_t *v_cache,
-                                const int *block_tables, const int *ctx_lens, int S, int nq, int nkv, int hd,
-                                int max_blocks, int block_size, float scale, float *part_o, float *part_ml,
-                                int part_size, int max_parts) {
+void decode_launch(bf16_t *out, const bf16_t *q, const bf16_t *k_new, const bf16_t *v_new, const int *slots,
+                   bf16_t *k_cache, bf16_t *v_cache, const int *block_tables, const int *ctx_lens, int S, int nq,
+                   int nkv, int hd, int max_blocks, int block_size, float scale, float *part_o, float *part_ml,
+                   int part_size, int max_parts) {
     if (S <= 0) return;
     if (hd != HD) {
         fprintf(stderr, "[llmgen-hip] attn_decode: only head_dim=128 is supported (got %d)\n", hd);
@@ -498,10 +528,40 @@ extern "C" void hip_attn_decode(bf16_t *out, const bf16_t *q, const bf16_t *k_ca
     DecodeArgs a{out, q, k_cache, v_cache, block_tables, ctx_lens, nq, nkv, max_blocks, block_size,
                  (block_size & (block_size - 1)) == 0 ? __builtin_ctz(block_size) : -1, scale * LLMGEN_LOG2E,
                  part_o, part_ml, part_size * k, max_parts, nparts, counters};
+    a.k_new = k_new;
+    a.v_new = v_new;
+    a.slots = slots;
+    a.kc_w = k_cache;
+    a.vc_w = v_cache;
     launch_decode_rows(dim3(nkv, S, nparts), a, G);
     if (!counters)  // batches beyond the counter array merge in a second kernel
         hipLaunchKernelGGL(attn_decode_reduce_kernel, dim3(nkv, S), dim3(DEC_THREADS), 0, g_llmgen_stream, out,
                            part_o, part_ml, ctx_lens, nq, G, a.span, nparts, max_parts);
+}
+
+}  // namespace
+
+extern "C" void hip_attn_decode(bf16_t *out, const bf16_t *q, const bf16_t *k_cache, const bf16_t *v_cache,
+                                const int *block_tables, const int *ctx_lens, int S, int nq, int nkv, int hd,
+                                int max_blocks, int block_size, float scale, float *part_o, float *part_ml,
+                                int part_size, int max_parts) {
+    decode_launch(out, q, nullptr, nullptr, nullptr, const_cast<bf16_t *>(k_cache), const_cast<bf16_t *>(v_cache),
+                  block_tables, ctx_lens, S, nq, nkv, hd, max_blocks, block_size, scale, part_o, part_ml, part_size,
+                  max_parts);
+}
+
+// store_kv of the step's one token per sequence fused into the decode launch (one kernel instead of two).
+extern "C" void hip_attn_decode_store_kv(bf16_t *out, const bf16_t *q, const bf16_t *k, const bf16_t *v,
+                                         const int *slot_mapping, bf16_t *k_cache, bf16_t *v_cache,
+                                         const int *block_tables, const int *ctx_lens, int S, int nq, int nkv, int hd,
+                                         int max_blocks, int block_size, float scale, float *part_o, float *part_ml,
+                                         int part_size, int max_parts) {
+    if (S > 0 && (k == nullptr || v == nullptr || slot_mapping == nullptr)) {
+        fprintf(stderr, "[llmgen-hip] attn_decode_store_kv: k, v and slot_mapping are required\n");
+        return;
+    }
+    decode_launch(out, q, k, v, slot_mapping, k_cache, v_cache, block_tables, ctx_lens, S, nq, nkv, hd, max_blocks,
+                  block_size, scale, part_o, part_ml, part_size, max_parts);
 }
 
 // Decode rows of a prefill / mixed step (segments with q_len == 1): one workgroup per (kv head, tile) streams the

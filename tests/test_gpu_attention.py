@@ -82,6 +82,56 @@ def test_decode_part_size_sweep(gpu, part_size):
     compare(to_u16(out), of, f"kt_decode ps={part_size}")
 
 
+@pytest.mark.parametrize("name,pad", [("c2", 0), ("c2", 5), ("kt_decode", 0), ("gqa8d", 3), ("c1", 0)])
+def test_fused_decode_store_kv_equals_unfused(gpu, name, pad):
+    """hip_attn_decode_store_kv == hip_store_kv then hip_attn_decode, bit for bit (output and both caches),
+    including graph-bucket padding rows (ctx 0, slot -1)."""
+    import copy as _copy
+    from llmgen_amd import step as S
+
+    wl = _copy.copy(make(name))
+    wl.pad_rows = pad
+    print(f"[gpu-test] fused decode {name} pad={pad}", flush=True)
+    t = wl.tensors(device="cuda")
+    meta = wl.meta(64)
+    assert meta.decode
+    dev = t["q"].device
+    n = meta.n_tok
+    q = torch.zeros((n, wl.nq, wl.hd), dtype=torch.bfloat16, device=dev)
+    k = torch.zeros((n, wl.nkv, wl.hd), dtype=torch.bfloat16, device=dev)
+    v = torch.zeros_like(k)
+    m = t["q"].shape[0]
+    q[:m], k[:m], v[:m] = t["q"], t["k"], t["v"]
+    d = lambda a: torch.from_numpy(a).to(dev)  # noqa: E731
+    slots, bt, ctx = d(meta.slots), d(meta.block_tables), d(meta.ctx)
+    ps, mp = S.part_size(n), S.max_parts(n, wl.max_model_len)
+    L = lib()
+    outs, caches = [], []
+    for fused in (False, True):
+        kc, vc = t["kc"].clone(), t["vc"].clone()
+        po = torch.empty(n * wl.nq * mp * wl.hd, dtype=torch.float32, device=dev)
+        pml = torch.empty(n * wl.nq * mp * 2, dtype=torch.float32, device=dev)
+        out = torch.full((n, wl.nq, wl.hd), float("nan"), dtype=torch.bfloat16, device=dev)
+        common = (bt.data_ptr(), ctx.data_ptr(), n, wl.nq, wl.nkv, wl.hd, wl.max_blocks, wl.block_size, wl.scale,
+                  po.data_ptr(), pml.data_ptr(), ps, mp)
+        if fused:
+            L.hip_attn_decode_store_kv(out.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), slots.data_ptr(),
+                                       kc.data_ptr(), vc.data_ptr(), *common)
+        else:
+            L.hip_store_kv(k.data_ptr(), v.data_ptr(), slots.data_ptr(), kc.data_ptr(), vc.data_ptr(), n, wl.nkv,
+                           wl.hd, wl.block_size)
+            L.hip_attn_decode(out.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(), *common)
+        torch.cuda.synchronize()
+        check_hip_error(f"fused={fused}")
+        outs.append(to_u16(out))
+        caches.append((to_u16(kc), to_u16(vc)))
+    np.testing.assert_array_equal(outs[1], outs[0])
+    assert_cache_equal(caches[1][0], caches[0][0], "fused K cache")
+    assert_cache_equal(caches[1][1], caches[0][1], "fused V cache")
+    if pad:
+        assert not outs[1][m:].any(), "padding rows not zero"
+
+
 @pytest.mark.parametrize("name", ["c3", "c4", "c5d", "c5p"])
 def test_step_matches_oracle_sampled_rows(gpu, name):
     wl = make(name)
