@@ -6,7 +6,7 @@
 // part_ml [S, nq, max_parts, 2] f32 owned by the caller, part p covering tokens [p*part_size, (p+1)*part_size).
 // Output: bf16(softmax(scale * q K^T) V) per (s, head), 0 for ctx <= 0 (cpu/attention.zig:80-83).
 //
-// Design (one workgroup = one (kv head, sequence, part), 4 waves):
+// Design (one workgroup = one (kv head, sequence, span of parts), 4 or 8 waves):
 //   * every wave owns 16-token tiles of the part; per round a wave issues all of its K and V loads at once as
 //     16-byte vectors (K: the MFMA B-operand layout, 16 tokens x 64 B per instruction; V: 4 full 256-byte rows
 //     per instruction), so a workgroup keeps up to 128 KB in flight;
@@ -45,8 +45,8 @@ __device__ __forceinline__ int blk_index(int t, int block_size, int bs_shift) {
 // tokens).  Each workgroup streams `span` tokens of one (kv head, sequence) pair: round r+1's block-table and
 // K/V loads are issued before round r is computed (register double buffering), so every wave keeps one round
 // of loads in flight while it computes.
-template <int G, int NT, bool POW2, bool PIPE, bool FUSE>
-__global__ void __launch_bounds__(DEC_THREADS) __attribute__((amdgpu_waves_per_eu(G >= 16 ? 1 : (PIPE || G >= 8 ? 2 : (G >= 4 ? 3 : 4)))))
+template <int G, int NT, bool POW2, bool PIPE, bool FUSE, int W>
+__global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(G >= 16 ? 1 : (PIPE || G >= 8 ? 2 : (G >= 4 ? 3 : 4)))))
     attn_decode_split_kernel(bf16_t *__restrict__ out, float *__restrict__ part_o, float *__restrict__ part_ml,
                              const bf16_t *__restrict__ q, const bf16_t *__restrict__ kc,
                              const bf16_t *__restrict__ vc, const int *__restrict__ block_tables,
@@ -57,7 +57,8 @@ __global__ void __launch_bounds__(DEC_THREADS) __attribute__((amdgpu_waves_per_e
                              const bf16_t *__restrict__ v_new, const int *__restrict__ slots,
                              bf16_t *__restrict__ kc_w, bf16_t *__restrict__ vc_w) {
     constexpr int WTOK = NT * 16;              // tokens per wave per round
-    constexpr int RTOK = DEC_WAVES * WTOK;     // tokens per round
+    constexpr int RTOK = W * WTOK;             // tokens per round
+    constexpr int NTH = 64 * W;
     const int kvh = blockIdx.x, part = blockIdx.z;
     // decode launch: blockIdx.y is the sequence and its query row.  Prefill-metadata launch (cu_q != null):
     // blockIdx.y is a query tile; only single-row segments (decode rows of a mixed step) are handled here.
@@ -87,7 +88,7 @@ __global__ void __launch_bounds__(DEC_THREADS) __attribute__((amdgpu_waves_per_e
     }
     if (t0 >= ctx) {
         if (ctx <= 0 && part == 0) {  // padding row: zeros (cpu/attention.zig:80-83)
-            for (int idx = threadIdx.x; idx < G * HD; idx += DEC_THREADS)
+            for (int idx = threadIdx.x; idx < G * HD; idx += NTH)
                 out[((long)row * nq + (long)kvh * G + idx / HD) * HD + idx % HD] = 0;
         }
         return;
@@ -98,11 +99,11 @@ __global__ void __launch_bounds__(DEC_THREADS) __attribute__((amdgpu_waves_per_e
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 15, rgrp = lane >> 4;
 
-    __shared__ float p_lds[DEC_WAVES][WTOK][G];
-    __shared__ float corr_lds[DEC_WAVES][G];
-    __shared__ float o_lds[DEC_WAVES][G][HD];
-    __shared__ float m_lds[DEC_WAVES][G];
-    __shared__ float l_lds[DEC_WAVES][G];
+    __shared__ float p_lds[W][WTOK][G];
+    __shared__ float corr_lds[W][G];
+    __shared__ float o_lds[W][G][HD];
+    __shared__ float m_lds[W][G];
+    __shared__ float l_lds[W][G];
 
     const int *bt = block_tables + (long)s * max_blocks;
     const long blk_stride = (long)nkv * block_size * HD;
@@ -304,14 +305,14 @@ __global__ void __launch_bounds__(DEC_THREADS) __attribute__((amdgpu_waves_per_e
     __syncthreads();
 
     // ---- merge the waves (LDS split-K merge) ----
-    for (int idx = tid; idx < G * HD; idx += DEC_THREADS) {
+    for (int idx = tid; idx < G * HD; idx += NTH) {
         const int g = idx / HD, d = idx % HD;
         float M = m_lds[0][g];
 #pragma unroll
-        for (int w = 1; w < DEC_WAVES; ++w) M = fmaxf(M, m_lds[w][g]);
+        for (int w = 1; w < W; ++w) M = fmaxf(M, m_lds[w][g]);
         float acc = 0.f, L = 0.f;
 #pragma unroll
-        for (int w = 0; w < DEC_WAVES; ++w) {
+        for (int w = 0; w < W; ++w) {
             const float e = fast_exp2(m_lds[w][g] - M);
             acc += e * o_lds[w][g][d];
             L += e * l_lds[w][g];
@@ -351,7 +352,7 @@ __global__ void __launch_bounds__(DEC_THREADS) __attribute__((amdgpu_waves_per_e
     if (tid == 0) s_last = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == np - 1;
     __syncthreads();
     if (!s_last) return;
-    for (int idx = tid; idx < G * HD; idx += DEC_THREADS) {
+    for (int idx = tid; idx < G * HD; idx += NTH) {
         const int g = idx / HD, d = idx % HD;
         const long h = (long)kvh * G + g;
         float *ml = part_ml + ((long)s * nq + h) * max_parts * 2;
@@ -420,17 +421,26 @@ struct DecodeArgs {
     const bf16_t *k_new = nullptr, *v_new = nullptr;  // fused KV write of this step's token (decode launch)
     const int *slots = nullptr;
     bf16_t *kc_w = nullptr, *vc_w = nullptr;
+    int waves = 4;  // waves per workgroup (4 or 8)
 };
 
-template <int G, int NT, bool POW2, bool PIPE>
-void launch_split(dim3 grid, const DecodeArgs &a) {
-    auto kern = a.k_new ? attn_decode_split_kernel<G, NT, POW2, PIPE, true>
-                        : attn_decode_split_kernel<G, NT, POW2, PIPE, false>;
-    hipLaunchKernelGGL(kern, grid, dim3(DEC_THREADS), 0,
+template <int G, int NT, bool POW2, bool PIPE, int W>
+void launch_split_w(dim3 grid, const DecodeArgs &a) {
+    auto kern = a.k_new ? attn_decode_split_kernel<G, NT, POW2, PIPE, true, W>
+                        : attn_decode_split_kernel<G, NT, POW2, PIPE, false, W>;
+    hipLaunchKernelGGL(kern, grid, dim3(64 * W), 0,
                        a.stream ? a.stream : g_llmgen_stream, a.out,
                        a.part_o, a.part_ml, a.q, a.kc, a.vc, a.bt, a.ctx, a.nq, a.nkv, a.max_blocks, a.block_size,
                        a.bs_shift, a.sl2, a.span, a.max_parts, a.nparts, a.counters, a.cu_q, a.tile_seq, a.k_new,
                        a.v_new, a.slots, a.kc_w, a.vc_w);
+}
+
+template <int G, int NT, bool POW2, bool PIPE>
+void launch_split(dim3 grid, const DecodeArgs &a) {
+    if (!PIPE && G <= 4 && a.waves == 8)
+        launch_split_w<G, NT, POW2, PIPE, 8>(grid, a);
+    else
+        launch_split_w<G, NT, POW2, PIPE, 4>(grid, a);
 }
 
 template <int G, int NT>
@@ -482,11 +492,24 @@ int num_compute_units() {
     return n;
 }
 
-void launch_decode_rows(dim3 grid, const DecodeArgs &a, int G) {
-    // single-buffered rounds at 3-4 waves per SIMD measure faster than register double buffering at 2 (c2,
-    // c5d); GQA groups of 8+ need the registers for o anyway
+// single-buffered rounds at 3-4 waves per SIMD measure faster than register double buffering at 2 (c2, c5d);
+// GQA groups of 8+ need the registers for o anyway
+bool use_pipe(int G) {
     static const int pipe_env = env_int("LLMGEN_DECODE_PIPE", -1);
-    const bool pipe = pipe_env >= 0 ? pipe_env != 0 : G >= 8;
+    return pipe_env >= 0 ? pipe_env != 0 : G >= 8;
+}
+
+// Waves per workgroup: 8 when the launch has enough (sequence, kv head) pairs to fill the chip with 8-wave
+// workgroups (fewer, longer workgroups: less split-K merging, fewer partial results), else 4.
+int decode_waves(int G, long pairs) {
+    static const int forced = env_int("LLMGEN_DECODE_WAVES", 0);
+    if (use_pipe(G) || G > 4) return 4;
+    if (forced == 4 || forced == 8) return forced;
+    return pairs * 2 >= num_compute_units() ? 8 : 4;
+}
+
+void launch_decode_rows(dim3 grid, const DecodeArgs &a, int G) {
+    const bool pipe = use_pipe(G);
     switch (G) {
         case 1: launch_pow2<1, 2>(grid, a, pipe); break;
         case 2: launch_pow2<2, 2>(grid, a, pipe); break;
@@ -517,11 +540,13 @@ void decode_launch(bf16_t *out, const bf16_t *q, const bf16_t *k_new, const bf16
         return;
     }
     // Each workgroup takes k consecutive parts (span = k * part_size tokens, one partial result).  k grows
-    // with the launch so that a long-context launch has about 2 workgroups per compute unit, each streaming
-    // a long span with its loads pipelined, instead of many short workgroups; partial slots stay < max_parts.
+    // with the launch so that a long-context launch has about 8 waves per compute unit (two 4-wave or one
+    // 8-wave workgroup), each streaming a long span, instead of many short workgroups; partial slots stay
+    // < max_parts.
     const long total = (long)nkv * S * max_parts;
     static const int wg_per_cu = env_int("LLMGEN_DECODE_WG_PER_CU", 2);
-    const long target = (long)wg_per_cu * num_compute_units();
+    const int W = decode_waves(G, (long)S * nkv);
+    const long target = (long)wg_per_cu * num_compute_units() * 4 / W;
     const int k = (int)(total > target ? total / target : 1);
     const int nparts = (max_parts + k - 1) / k;
     int *counters = (long)S * nkv <= MAX_MERGE_SEGMENTS ? merge_counters() : nullptr;
@@ -533,6 +558,7 @@ void decode_launch(bf16_t *out, const bf16_t *q, const bf16_t *k_new, const bf16
     a.slots = slots;
     a.kc_w = k_cache;
     a.vc_w = v_cache;
+    a.waves = W;
     launch_decode_rows(dim3(nkv, S, nparts), a, G);
     if (!counters)  // batches beyond the counter array merge in a second kernel
         hipLaunchKernelGGL(attn_decode_reduce_kernel, dim3(nkv, S), dim3(DEC_THREADS), 0, g_llmgen_stream, out,
@@ -575,6 +601,7 @@ void llmgen_decode_rows_of_prefill(bf16_t *out, const bf16_t *q, const bf16_t *k
     DecodeArgs a{out, q, k_cache, v_cache, block_tables, ctx_lens, nq, nkv, max_blocks, block_size,
                  (block_size & (block_size - 1)) == 0 ? __builtin_ctz(block_size) : -1, scale * LLMGEN_LOG2E,
                  nullptr, nullptr, 1 << 30, 1, 1, nullptr, cu_q, tile_seq, stream};
+    a.waves = decode_waves(G, (long)n_tiles * nkv);
     launch_decode_rows(dim3(nkv, n_tiles, 1), a, G);
 }
 
