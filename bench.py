@@ -2,9 +2,9 @@
 """Benchmark of the MI355X attention path on BASELINE's configurations (1 GPU).
 
 A step is one layer's attention step of configuration c2 (32-sequence batched decode, the configuration the
-metric is quoted on): store_kv of the step's K/V plus split-K paged decode.  As in the engine, the decode step
-is a hipGraph bucket holding every decoder layer (28 for Qwen3-0.6B, each with its own KV pools); the bench
-replays it and reports graph time / 28 per step.  ``value`` = algorithmic decode bytes (sum ctx * nkv * hd * 2 B * 2 + q + out)
+metric is quoted on): store_kv of the step's K/V plus split-K paged decode (one fused launch).  As in the engine,
+the decode step is a hipGraph bucket holding every decoder layer (28 for Qwen3-0.6B, each with its own KV pools),
+captured by the C++ executor slice; the bench replays it and reports graph time / 28 per step.  ``value`` = algorithmic decode bytes (sum ctx * nkv * hd * 2 B * 2 + q + out)
 per step / step time, in GB/s.  The other configurations are reported under ``extra``: decode GB/s for c1 and
 c5d, prefill TFLOP/s (4 * hd * nq * causal pairs / time) for c3 and c5p, and the mixed step c4.
 
@@ -250,32 +250,35 @@ def main() -> int:
         print(json.dumps({"config": args.only, "attn_us": round(ms * 1e3, 2)}), flush=True)
         return 0
 
-    # ---- the metric step: c2 decode, store_kv + decode replayed from a hipGraph bucket ----
-    from llmgen_amd.graphs import DecodeGraphs
+    # ---- the metric step: c2 decode (store_kv fused into split-K decode), replayed from a hipGraph bucket
+    #      captured by the C++ executor slice (llmgen_graphs_*, the engine's captureGraphs / replay) ----
+    from llmgen_amd import host as H
 
     st = Step("c2")
     wl = st.wl
     # the engine's decode graph holds every decoder layer: N_LAYERS attention steps, each with its own KV pools
-    from llmgen_amd import attention as A
-
-    layers = [st.layer] + [A.LayerState(st.t["kc"].clone(), st.t["vc"].clone()) for _ in range(N_LAYERS - 1)]
-    graphs = DecodeGraphs(layers, wl.nq, wl.nkv, wl.hd, wl.block_size, wl.max_blocks, wl.max_model_len,
-                          max_seqs=len(wl.entries), buckets=[len(wl.entries)])
-    b = graphs.prepare(wl.entries, st.t["q"], st.t["k"], st.t["v"])
+    kcs = [st.layer.k] + [st.t["kc"].clone() for _ in range(N_LAYERS - 1)]
+    vcs = [st.layer.v] + [st.t["vc"].clone() for _ in range(N_LAYERS - 1)]
+    graphs = H.Graphs(kcs, vcs, wl.nq, wl.nkv, wl.hd, wl.block_size, wl.max_model_len, max_seqs=len(wl.entries),
+                      buckets=[len(wl.entries)])
+    rng = np.random.default_rng(0)
+    seqs = [H.Sequence_(rng.integers(0, 1000, e.q_start + e.q_len).tolist(), list(e.block_table))
+            for e in wl.entries]
+    ents = [(i, e.q_start, e.q_len) for i, e in enumerate(wl.entries)]
+    graphs.step(seqs, ents, st.t["q"], st.t["k"], st.t["v"], st.out)  # metadata upload + q/k/v + one replay
     for _ in range(args.warmup):
-        graphs.launch(b)
+        graphs.replay()
     torch.cuda.synchronize()
     L = st.L
     e0, e1 = _timer_pair()
     torch.cuda.synchronize()  # barrier (one rank) + synchronize
     L.hip_timer_record(e0)
     for _ in range(args.steps):
-        graphs.launch(b)
+        graphs.replay()
     L.hip_timer_record(e1)
     graph_ms = L.hip_timer_elapsed_ms(e0, e1) / args.steps
     torch.cuda.synchronize()
     step_ms = graph_ms / N_LAYERS  # one layer's attention step
-    st.out.copy_(b.out[: len(wl.entries)])
     value = wl.decode_bytes() / (step_ms * 1e-3) / 1e9
 
     # ---- dominant kernel launch: hip_attn_decode alone (split-K partials + merge), events on its stream ----
@@ -307,8 +310,8 @@ def main() -> int:
         "ms_per_step": round(step_ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16", "data": "synthetic (seeded N(0,1) bf16 q/k/v and KV history, random block tables)",
         "config": {"workload": "c2: batched decode, 32 seqs, ctx~U[128,1024], 16q/8kv/hd128, block 256; step = one "
-                               "layer's store_kv + split-K decode, timed inside a 28-layer hipGraph decode bucket "
-                               "(graph time / 28)",
+                               "layer's store_kv + split-K decode (one fused launch), timed inside a 28-layer "
+                               "hipGraph decode bucket captured by the C++ executor slice (graph time / 28)",
                    "graph_ms": round(graph_ms, 4), "layers_per_graph": N_LAYERS,
                    "hbm_frac": round(value / HBM_PEAK_GBS, 4), "parallelism": "single GPU"},
         "roofline": roofline,

@@ -2,7 +2,7 @@
  * llmgen_model.h -- C-ABI of the non-attention ops the Qwen3 forward needs around the attention path, in
  * libllmgen_attn.so.  They exist for the end-to-end greedy-token check, not as tuned kernels: each one computes
  * every output value in the same order and with the same roundings as the reference CPU backend
- * (src/backend/cpu/*.zig), so that a forward built from them differs from the CPU backend's only through the
+ * (the src/backend/cpu/ ops), so that a forward built from them differs from the CPU backend's only through the
  * attention kernels.  Each entry point replaces one extern of the reference CUDA backend with the same argument
  * list (citations relative to the reference repository root):
  *   hip_embedding    src/backend/cuda/embedding/embedding.zig:7      (CPU: src/backend/cpu/embedding.zig)

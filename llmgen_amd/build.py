@@ -1,7 +1,7 @@
 """Build the gfx950 attention library in-tree: llmgen_amd/libllmgen_attn.so.
 
-Every ``csrc/*.hip`` file is compiled with hipcc for gfx950 only and linked into one shared library whose C-ABI is
-declared in ``include/llmgen_attn.h``.  Packed FP32 instructions are disabled for all device code
+Every ``csrc/*.hip`` and ``csrc/*.cpp`` file is compiled with hipcc for gfx950 only and linked into one shared
+library whose C-ABI is declared in ``include/*.h``.  Packed FP32 instructions are disabled for all device code
 (``-target-feature -packed-fp32-ops``).  Run ``python -m llmgen_amd.build`` or call :func:`build`.
 """
 from __future__ import annotations
@@ -19,8 +19,10 @@ LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
+INCLUDE = os.path.join(os.path.dirname(PKG_DIR), "include")
 COMMON_FLAGS = [
     f"--offload-arch={ARCH}",
+    f"-I{INCLUDE}",
     "-O3",
     "-fPIC",
     "-std=c++17",
@@ -42,11 +44,12 @@ def _compile(src: str, obj: str) -> None:
 
 
 def build(verbose: bool = True) -> str:
-    """Compile every csrc/*.hip and link libllmgen_attn.so. Returns the library path."""
-    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+    """Compile every csrc/*.hip (device code) and csrc/*.cpp (host executor slice) and link libllmgen_attn.so.
+    Returns the library path."""
+    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")) + glob.glob(os.path.join(CSRC, "*.cpp")))
     obj_dir = os.path.join(PKG_DIR, "_build")
     os.makedirs(obj_dir, exist_ok=True)
-    objs = [os.path.join(obj_dir, os.path.basename(s)[:-4] + ".o") for s in srcs]
+    objs = [os.path.join(obj_dir, os.path.splitext(os.path.basename(s))[0] + ".o") for s in srcs]
     with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
         list(ex.map(lambda so: _compile(*so), zip(srcs, objs)))
     tmp = LIB_PATH + ".tmp"

@@ -437,7 +437,7 @@ void launch_split_w(dim3 grid, const DecodeArgs &a) {
 
 template <int G, int NT, bool POW2, bool PIPE>
 void launch_split(dim3 grid, const DecodeArgs &a) {
-    if (!PIPE && G <= 4 && a.waves == 8)
+    if (G <= 4 && a.waves == 8)
         launch_split_w<G, NT, POW2, PIPE, 8>(grid, a);
     else
         launch_split_w<G, NT, POW2, PIPE, 4>(grid, a);
@@ -503,7 +503,7 @@ bool use_pipe(int G) {
 // workgroups (fewer, longer workgroups: less split-K merging, fewer partial results), else 4.
 int decode_waves(int G, long pairs) {
     static const int forced = env_int("LLMGEN_DECODE_WAVES", 0);
-    if (use_pipe(G) || G > 4) return 4;
+    if (G > 4) return 4;
     if (forced == 4 || forced == 8) return forced;
     return pairs * 2 >= num_compute_units() ? 8 : 4;
 }

@@ -115,16 +115,18 @@ def _declared_symbols():
     for header in sorted(glob.glob(os.path.join(ROOT, "include", "*.h"))):
         with open(header) as f:
             text = re.sub(r"/\*.*?\*/", "", f.read(), flags=re.S)
-        names.update(re.findall(r"\b(hip_\w+)\s*\(", text))
+        names.update(re.findall(r"\b((?:hip|llmgen)_\w+)\s*\(", text))
     return sorted(names)
 
 
 def test_library_exports_every_declared_symbol():
     from llmgen_amd._lib import SIGNATURES, lib
 
+    from llmgen_amd.host import HOST_SIGNATURES
+
     declared = _declared_symbols()
     assert len(declared) >= 25
-    assert sorted(SIGNATURES) == declared, "ctypes signatures out of sync with the header"
+    assert sorted(list(SIGNATURES) + list(HOST_SIGNATURES)) == declared, "ctypes signatures out of sync with headers"
     L = lib()  # loads without a GPU
     for name in declared:
         assert hasattr(L, name), f"{name} not exported"
