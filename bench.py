@@ -188,6 +188,17 @@ def cpu_baseline(st: "Step", budget_s: float = 10.0) -> dict:
         if el >= budget_s:
             break
     per = el / reps
+    # the same step on all host cores the box gives this job (OpenMP over (token, head)), for scale
+    n_thr = min(16, os.cpu_count() or 1)
+    rows = np.arange(int(meta.cu_q[-1]), dtype=np.int32)
+    reps_mt, t1 = 0, time.perf_counter()
+    while True:
+        oracle.attend_rows(*args, rows=rows, threads=n_thr)
+        reps_mt += 1
+        el_mt = time.perf_counter() - t1
+        if el_mt >= budget_s / 4:
+            break
+    per_mt = el_mt / reps_mt
     # parity of the GPU output of the same step (already computed by the benchmark's warm-up)
     got = oracle.bf16_to_f32(to_u16(st.out)).astype(np.float64)
     err = float(np.abs(got - of).max())
@@ -196,6 +207,8 @@ def cpu_baseline(st: "Step", budget_s: float = 10.0) -> dict:
         "value": round(wl.decode_bytes() / per / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
         "sample": f"full c2 decode step (32 seqs, all heads) x{reps} reps, {per * 1e3:.1f} ms/step, oracle/attend",
         "gpu_vs_oracle": {"max_abs": round(err, 5), "rel_l2": round(rel, 5)},
+        "multicore": {"value": round(wl.decode_bytes() / per_mt / 1e9, 4), "unit": "GB/s", "cores": n_thr,
+                      "sample": f"same step x{reps_mt} reps, {per_mt * 1e3:.1f} ms/step, OpenMP over (token, head)"},
     }
 
 
