@@ -247,3 +247,52 @@ def test_mixed_step_graph_capture(gpu):
             A.g_attn_mgr = mgr
     finally:
         L.hip_graph_destroy(g)
+
+
+# ---------------------------------------------------------------- full-size properties
+def _step(wl, t):
+    """store_kv + attention of wl through PagedAttentionImpl on tensors t (not modified); returns out, kc, vc."""
+    return run_gpu(wl, t)
+
+
+def test_c5d_block_permutation_invariance(gpu):
+    """Full c5d (16 x 32768 keys): relabelling the physical blocks (pool rows moved, tables mapped the same way)
+    leaves the decode output bit-identical and moves the written KV rows with it."""
+    import copy as _copy
+
+    from llmgen_amd.step import Entry
+
+    wl = make("c5d")
+    print("[gpu-test] c5d permutation", flush=True)
+    t = wl.tensors(device="cuda")
+    out0, kc0, vc0 = _step(wl, t)
+    perm = np.random.default_rng(9).permutation(wl.num_blocks)  # physical block b -> perm[b]
+    inv = torch.from_numpy(np.argsort(perm)).to("cuda")
+    t2 = dict(t)
+    t2["kc"], t2["vc"] = t["kc"][inv], t["vc"][inv]  # new pool row perm[b] holds old block b
+    wl2 = _copy.copy(wl)
+    wl2.entries = [Entry(e.q_start, e.q_len, [int(perm[b]) for b in e.block_table]) for e in wl.entries]
+    out1, kc1, vc1 = _step(wl2, t2)
+    np.testing.assert_array_equal(to_u16(out1), to_u16(out0))
+    assert_cache_equal(to_u16(kc1), to_u16(kc0[inv]), "permuted K cache")
+    assert_cache_equal(to_u16(vc1), to_u16(vc0[inv]), "permuted V cache")
+
+
+def test_c5p_chunked_prefill_equals_tail(gpu):
+    """Full c5p (16384-token prompt): prefilling the last 4096 tokens as a chunk against the cached first 12288
+    gives exactly the last 4096 rows of the full prefill (each row's keys, order and arithmetic are the same)."""
+    import copy as _copy
+
+    from llmgen_amd.step import Entry
+
+    wl = make("c5p")
+    print("[gpu-test] c5p chunk", flush=True)
+    t = wl.tensors(device="cuda")
+    out_full, kc, vc = _step(wl, t)
+    L, tail = wl.entries[0].q_len, 4096
+    wl2 = _copy.copy(wl)
+    wl2.entries = [Entry(L - tail, tail, wl.entries[0].block_table)]
+    t2 = {"q": t["q"][L - tail:].contiguous(), "k": t["k"][L - tail:].contiguous(),
+          "v": t["v"][L - tail:].contiguous(), "kc": kc, "vc": vc}
+    out_chunk, _, _ = _step(wl2, t2)
+    np.testing.assert_array_equal(to_u16(out_chunk), to_u16(out_full)[L - tail:])
