@@ -221,6 +221,20 @@ def make(name: str, seed: Optional[int] = None) -> Workload:
         tables, nb = _tables(rng, ctxs, 32, permute=True, extra_blocks=3)
         return Workload(name, nq, nkv, 128, 32, nb, 48, 1536, _decode_entries(ctxs, tables), std=1.0, seed=s,
                         note=f"decode step at GQA {nq // nkv}")
+    if name in ("bs48", "bs48d"):
+        # a block size that is not a power of two (the kernels' generic block-table path), GQA 4
+        s = 41 if seed is None else seed
+        rng = np.random.default_rng(s)
+        if name == "bs48":
+            spec = [(100, 170), (0, 97), (47, 1), (0, 1)]
+        else:
+            spec = [(c - 1, 1) for c in (48, 49, 1000, 2, 385)]
+        ctxs = [a + b for a, b in spec]
+        tables, nb = _tables(rng, ctxs, 48, permute=True, extra_blocks=2)
+        ents = [Entry(a, b, t) for (a, b), t in zip(spec, tables)]
+        return Workload(name, 16, 4, 128, 48, nb, 24, 1152, ents, std=1.0, seed=s,
+                        decode=None if name == "bs48d" else False,
+                        note=f"block size 48, GQA 4 ({'decode' if name == 'bs48d' else 'mixed'})")
     raise KeyError(name)
 
 
