@@ -5,9 +5,12 @@ head split -> per-head q/k RMSNorm -> NEOX RoPE at ``g_step.pos`` -> paged atten
 decode or causal varlen prefill) -> output projection -> residual add; RMSNorm -> SwiGLU MLP -> residual add;
 then the final RMSNorm, gather of each sequence's last row, the tied LM head and sampling.
 
-Attention runs through :class:`llmgen_amd.attention.PagedAttentionImpl` exactly as the engine drives it.  Every
-other op is a ``include/llmgen_model.h`` kernel that computes each value in the reference CPU backend's order and
-rounding, so a forward here differs from the CPU backend's only through the attention kernels.
+Each step is prepared and dispatched by the C++ executor slice (``include/llmgen_host.h``): ``llmgen_fill_meta``
+packs the step's metadata (token ids, positions, slots, ``cu_q``, ``ctx``, ``last``, temperatures, prefill tiles,
+block tables, step seed) into one buffer uploaded with one copy, ``llmgen_bind_step`` publishes its device
+addresses, and ``llmgen_paged_attention`` runs each layer's attention.  Every other op is an
+``include/llmgen_model.h`` kernel that computes each value in the reference CPU backend's order and rounding, so a
+forward here differs from the CPU backend's only through the attention kernels.
 
 Weights are random (no checkpoint is available offline): :func:`random_weights` draws a seeded Qwen3-0.6B-shaped
 set in GGUF tensor naming, bf16 for matrices and f32 for norm gains as GGUF stores them.
@@ -22,6 +25,7 @@ import numpy as np
 import torch
 
 from . import attention as A
+from . import host as Hx
 from . import step as stepmod
 from ._lib import lib
 
@@ -124,28 +128,34 @@ class Qwen3:
         cos_t, sin_t = rope_tables(cfg.max_model_len, cfg.head_dim, cfg.rope_theta)
         self.cos, self.sin = _bits(cos_t, device), _bits(sin_t, device)
         self.max_blocks = (cfg.max_model_len + cfg.block_size - 1) // cfg.block_size
-        A.g_attn_mgr = A.PagedAttentionManager()
-        for i in range(cfg.n_layers):
-            A.g_attn_mgr.reserve_layer(i, num_blocks, cfg.n_kv_head, cfg.block_size, cfg.head_dim, device)
-        meta_elems = (5 * max_tokens + 8 * max_seqs + 2 * (max_tokens // 64 + max_seqs)
-                      + max_seqs * self.max_blocks + 64)
-        self.ws = A.Workspace.allocate(cfg.n_head, cfg.head_dim, max_seqs, cfg.max_model_len, meta_elems, device)
-        self.max_seqs, self.max_tokens = max_seqs, max_tokens
-        self.sample_scratch = torch.empty(max(self.L.hip_sample_scratch_bytes(max_seqs), 4), dtype=torch.uint8,
-                                          device=device)
+        # paged KV pools, one pair per layer (memory/page_atten.zig:15-28)
+        self.kv = [A.PagedAttentionManager().reserve_layer(i, num_blocks, cfg.n_kv_head, cfg.block_size,
+                                                           cfg.head_dim, device) for i in range(cfg.n_layers)]
         self.pf_tile = self.L.hip_attn_prefill_tile()
+        # executor.zig:92-102 Workspace.of: metadata, split-K scratch, sampling scratch
+        ws = Hx.workspace(cfg.n_head, cfg.head_dim, max_seqs, max_tokens, cfg.max_model_len, cfg.block_size,
+                          self.pf_tile)
+        u8 = torch.uint8
+        self.meta_dev = torch.zeros(ws["meta"], dtype=u8, device=device)
+        self.part_o = torch.empty(max(ws["part_o"], 4), dtype=u8, device=device)
+        self.part_ml = torch.empty(max(ws["part_ml"], 4), dtype=u8, device=device)
+        self.sample_scratch = torch.empty(max(ws["sample"], 4), dtype=u8, device=device)
+        self.max_seqs, self.max_tokens = max_seqs, max_tokens
+        self.step_seed = 0
 
     # -- buffers of one step
     def _empty(self, *shape, dtype=torch.int16):
         return torch.empty(shape, dtype=dtype, device=self.device)
 
-    def forward(self, entries: Sequence[stepmod.Entry], ids: Sequence[int], temps=None, seed: int = 0,
+    def forward(self, entries: Sequence[stepmod.Entry], ids: Sequence[int], temps=None, seed=None,
                 fused_qk: bool = True) -> List[int]:
-        """``fused_qk`` runs q/k norm + RoPE + the KV write as one kernel (hip_qk_norm_rope_store_kv); the unfused
-        path runs the reference graph's five launches.  Both give identical values."""
+        """One step: entries[i] computes positions [q_start, q_start + q_len) of sequence i with this step's
+        token ids (concatenated in entry order).  ``temps[i]`` > 0 samples sequence i (Gumbel-max), else greedy.
+        ``seed`` resets the step-seed state (executor.zig:773 advances it every step).  ``fused_qk`` runs q/k norm
+        + RoPE + the KV write as one kernel (hip_qk_norm_rope_store_kv); the unfused path runs the reference
+        graph's five launches.  Both give identical values."""
         cfg, L = self.cfg, self.L
-        meta = stepmod.fill_meta(entries, cfg.block_size, self.max_blocks, self.pf_tile)
-        T, S = meta.n_tok, meta.n_seq
+        T, S = sum(e.q_len for e in entries), len(entries)
         if len(ids) != T or T > self.max_tokens or S > self.max_seqs:
             raise ValueError(f"step of {T} tokens / {S} sequences does not fit (ids {len(ids)})")
         if any(e.q_start + e.q_len > cfg.max_model_len for e in entries):
@@ -153,13 +163,26 @@ class Qwen3:
         ids_np = np.asarray(ids, np.int64)
         if ids_np.min() < 0 or ids_np.max() >= cfg.vocab:
             raise IndexError("token id out of range")
-        g = A.bind_step(meta, self.ws, cfg.n_head, cfg.n_kv_head, cfg.head_dim, cfg.block_size, self.max_blocks,
-                        cfg.max_model_len)
+        # the executor's view of the step: each sequence's token ids (this step's known), block table, temperature
+        seqs, ents, t = [], [], 0
+        for i, e in enumerate(entries):
+            tok = np.zeros(e.q_start + e.q_len, np.int32)
+            tok[e.q_start:] = ids_np[t:t + e.q_len]
+            t += e.q_len
+            seqs.append(Hx.Sequence_(tok, list(e.block_table), 0.0 if temps is None else float(temps[i])))
+            ents.append((i, e.q_start, e.q_len))
+        decode = all(e.q_len == 1 for e in entries)  # every entry ends its sequence, so it emits
+        n_tiles = 0 if decode else sum((e.q_len + self.pf_tile - 1) // self.pf_tile for e in entries)
+        if seed is not None:
+            self.step_seed = int(seed)
+        buf, lay, self.step_seed = Hx.fill_meta(seqs, ents, S, n_tiles, self.pf_tile, cfg.block_size,
+                                                self.max_blocks, self.step_seed)
+        self.meta_dev[:lay.total].copy_(torch.from_numpy(buf))  # one upload per step
+        g = Hx.bind_step(self.meta_dev.data_ptr(), lay, T, S, n_tiles, decode, cfg.n_head, cfg.n_kv_head,
+                         cfg.head_dim, cfg.block_size, self.max_blocks, cfg.max_model_len, self.part_o.data_ptr(),
+                         self.part_ml.data_ptr(), self.sample_scratch.data_ptr(), hidden=cfg.hidden)
         d = self.device
-        ids_d = torch.tensor(ids_np.astype(np.int32), device=d)
-        temps_d = torch.tensor(np.zeros(S, np.float32) if temps is None else np.asarray(temps, np.float32),
-                               device=d)
-        seed_d = torch.tensor([seed], dtype=torch.int64, device=d)
+        ids_ptr = self.meta_dev.data_ptr() + lay.ids
         H, nq, nkv, hd, F = cfg.hidden, cfg.n_head, cfg.n_kv_head, cfg.head_dim, cfg.ffn
         x = self._empty(T, H)
         xn, o = self._empty(T, H), self._empty(T, H)
@@ -168,15 +191,15 @@ class Qwen3:
         gate, up = self._empty(T, F), self._empty(T, F)
         p = lambda t: t.data_ptr()  # noqa: E731
         W = self.w
-        L.hip_embedding(p(x), p(ids_d), p(W["token_embd.weight"]), T, H)
+        L.hip_embedding(p(x), ids_ptr, p(W["token_embd.weight"]), T, H)
         for i in range(cfg.n_layers):
             b = f"blk.{i}."
             L.hip_rmsnorm(p(xn), p(x), p(W[b + "attn_norm.weight"]), T, H, cfg.rms_eps)
             L.hip_linear(p(q), 0, p(xn), p(W[b + "attn_q.weight"]), T, nq * hd, H)
             L.hip_linear(p(k), 0, p(xn), p(W[b + "attn_k.weight"]), T, nkv * hd, H)
             L.hip_linear(p(v), 0, p(xn), p(W[b + "attn_v.weight"]), T, nkv * hd, H)
+            kv = self.kv[i]
             if fused_qk:
-                kv = A.kv_of(i)
                 L.hip_qk_norm_rope_store_kv(p(q), p(kv.k), p(kv.v), p(q), p(k), p(v),
                                             p(W[b + "attn_q_norm.weight"]), p(W[b + "attn_k_norm.weight"]),
                                             cfg.rms_eps, p(self.cos), p(self.sin), g.pos, g.slots, T, nq, nkv, hd,
@@ -186,7 +209,7 @@ class Qwen3:
                 L.hip_rmsnorm(p(k), p(k), p(W[b + "attn_k_norm.weight"]), T * nkv, hd, cfg.rms_eps)
                 L.hip_rope(p(q), p(q), p(self.cos), p(self.sin), g.pos, T, nq, hd)
                 L.hip_rope(p(k), p(k), p(self.cos), p(self.sin), g.pos, T, nkv, hd)
-            A.PagedAttentionImpl.execute(0, A.AttnNode(data=attn, src=[q, k, v], layer_id=i), store_kv=not fused_qk)
+            Hx.paged_attention(g, attn, q, k, v, kv.k, kv.v, store_kv=not fused_qk)
             L.hip_linear(p(o), 0, p(attn), p(W[b + "attn_output.weight"]), T, H, nq * hd)
             L.hip_add(p(x), p(x), p(o), T * H)
             L.hip_rmsnorm(p(xn), p(x), p(W[b + "ffn_norm.weight"]), T, H, cfg.rms_eps)
@@ -202,6 +225,6 @@ class Qwen3:
         logits = self._empty(S, cfg.vocab)
         L.hip_linear(p(logits), 0, p(last), p(W["token_embd.weight"]), S, cfg.vocab, H)
         out = torch.empty(S, dtype=torch.int32, device=d)
-        L.hip_sample(p(out), p(logits), p(temps_d), p(seed_d), S, cfg.vocab, p(self.sample_scratch))
+        L.hip_sample(p(out), p(logits), g.temps, g.seed, S, cfg.vocab, p(self.sample_scratch))
         self.last_logits = logits
         return out.cpu().tolist()
