@@ -143,6 +143,34 @@ class Qwen3:
         self.max_seqs, self.max_tokens = max_seqs, max_tokens
         self.step_seed = 0
 
+    def execute(self, entries: Sequence[stepmod.Entry], ids: Sequence[int], temps=None) -> List[int]:
+        """executor.zig:986-1043: a step larger than max_tokens runs as several passes (an entry's query range may
+        be cut); the sampled id of an entry comes from the pass that reaches its end."""
+        total = sum(e.q_len for e in entries)
+        if total <= self.max_tokens:
+            return self.forward(entries, ids, temps)
+        starts = np.cumsum([0] + [e.q_len for e in entries])
+        pieces = Hx.plan_passes([(i, e.q_start, e.q_len) for i, e in enumerate(entries)], self.max_tokens)
+        out = [0] * len(entries)
+        by_pass = {}
+        for pas, owner, piece in pieces:
+            by_pass.setdefault(pas, []).append((owner, piece))
+        for pas in sorted(by_pass):
+            group = by_pass[pas]
+            ents, pids, ptemps = [], [], []
+            for owner, (_, q_start, q_len) in group:
+                e = entries[owner]
+                ents.append(stepmod.Entry(q_start, q_len, e.block_table))
+                off = starts[owner] + (q_start - e.q_start)
+                pids.extend(ids[off:off + q_len])
+                ptemps.append(0.0 if temps is None else temps[owner])
+            toks = self.forward(ents, pids, ptemps)
+            for (owner, (_, q_start, q_len)), tk in zip(group, toks):
+                e = entries[owner]
+                if q_start + q_len == e.q_start + e.q_len:
+                    out[owner] = tk
+        return out
+
     # -- buffers of one step
     def _empty(self, *shape, dtype=torch.int16):
         return torch.empty(shape, dtype=dtype, device=self.device)

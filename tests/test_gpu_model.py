@@ -252,3 +252,31 @@ def test_fused_qk_norm_rope_store_kv_matches_unfused(gpu, T, nq, nkv, bs, nb):
     O.store_kv(ko, v, slots, kc_o, vc_o, nkv, hd, bs)
     np.testing.assert_array_equal(down(kc_f), kc_o)
     np.testing.assert_array_equal(down(vc_f), vc_o)
+
+
+def test_qwen3_passes_over_max_tokens_match_one_pass(gpu):
+    """executor.zig:986-1043 on a small Qwen3-shaped model: a prefill step larger than max_tokens, split into
+    passes by the C++ planner (an entry's prompt cut across passes), samples the same ids, and leaves the same
+    logits for the final pass's rows, as one pass over the whole step."""
+    from llmgen_amd.qwen3 import Qwen3, Qwen3Config, random_weights
+
+    cfg = Qwen3Config(vocab=2048, hidden=256, n_layers=3, n_head=8, n_kv_head=4, head_dim=128, ffn=512,
+                      max_model_len=256, block_size=16)
+    W = random_weights(cfg, seed=4, std=0.05, embd_row_sigma=1.0)
+    rng = np.random.default_rng(6)
+    lens = [70, 33, 9]
+    tables = [list(range(0, 8)), list(range(8, 16)), list(range(16, 24))]
+    ids = rng.integers(0, cfg.vocab, sum(lens)).tolist()
+    ents = [S.Entry(0, n, tables[i]) for i, n in enumerate(lens)]
+    one = Qwen3(cfg, W, num_blocks=24, max_seqs=4, max_tokens=256)
+    ids_one = one.execute(ents, ids)
+    split = Qwen3(cfg, W, num_blocks=24, max_seqs=4, max_tokens=40)  # passes of <= 40 tokens
+    ids_split = split.execute(ents, ids)
+    check_err()
+    assert ids_split == ids_one, (ids_split, ids_one)
+    # both models now hold the same KV: a decode step on each gives the same ids and logits
+    dec = [S.Entry(n, 1, tables[i]) for i, n in enumerate(lens)]
+    nxt = [int(x) for x in ids_one]
+    a, b = one.forward(dec, nxt), split.forward(dec, nxt)
+    assert a == b
+    np.testing.assert_array_equal(down(one.last_logits), down(split.last_logits))
