@@ -296,3 +296,24 @@ def test_c5p_chunked_prefill_equals_tail(gpu):
           "v": t["v"][L - tail:].contiguous(), "kc": kc, "vc": vc}
     out_chunk, _, _ = _step(wl2, t2)
     np.testing.assert_array_equal(to_u16(out_chunk), to_u16(out_full)[L - tail:])
+
+
+def test_zero_sized_launches_are_noops(gpu):
+    """T <= 0, S <= 0 and n_tiles <= 0 launch nothing (the reference's degenerate-input contract), also for the
+    fused entry points; the output buffer is untouched and no error is raised."""
+    L = lib()
+    out = torch.full((4, 4, 128), 7.0, dtype=torch.bfloat16, device="cuda")
+    before = to_u16(out).copy()
+    dummy = torch.zeros(1 << 16, dtype=torch.int32, device="cuda").data_ptr()
+    p = out.data_ptr()
+    for n in (0, -3):
+        L.hip_store_kv(dummy, dummy, dummy, dummy, dummy, n, 2, 128, 16)
+        L.hip_attn_decode(p, dummy, dummy, dummy, dummy, dummy, n, 4, 2, 128, 4, 16, 0.1, dummy, dummy, 64, 4)
+        L.hip_attn_decode_store_kv(p, dummy, dummy, dummy, dummy, dummy, dummy, dummy, dummy, n, 4, 2, 128, 4, 16,
+                                   0.1, dummy, dummy, 64, 4)
+        L.hip_attn_prefill(p, dummy, dummy, dummy, dummy, dummy, dummy, dummy, dummy, n, 4, 2, 128, 4, 16, 0.1)
+        L.hip_qk_norm_rope_store_kv(p, dummy, dummy, dummy, dummy, dummy, dummy, dummy, 1e-6, dummy, dummy, dummy,
+                                    dummy, n, 4, 2, 128, 16)
+    torch.cuda.synchronize()
+    check_hip_error("zero-sized launches")
+    np.testing.assert_array_equal(to_u16(out), before)
