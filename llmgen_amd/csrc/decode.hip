@@ -32,8 +32,7 @@
 namespace {
 
 constexpr int HD = 128;
-constexpr int DEC_WAVES = 4;
-constexpr int DEC_THREADS = 64 * DEC_WAVES;
+constexpr int DEC_THREADS = 256;  // the separate merge kernel's workgroup
 
 // Block-table lookup of logical token t (POW2: block_size == 1 << bs_shift).
 template <bool POW2>
@@ -41,10 +40,10 @@ __device__ __forceinline__ int blk_index(int t, int block_size, int bs_shift) {
     return POW2 ? (t >> bs_shift) : (t / block_size);
 }
 
-// G = query heads per KV head (1..16); NT = 16-token tiles per wave per round (a round is 4 waves x 16*NT
-// tokens).  Each workgroup streams `span` tokens of one (kv head, sequence) pair: round r+1's block-table and
-// K/V loads are issued before round r is computed (register double buffering), so every wave keeps one round
-// of loads in flight while it computes.
+// G = query heads per KV head (1..16); NT = 16-token tiles per wave per round (a round is W waves x 16*NT
+// tokens); W = waves per workgroup (4 or 8); FUSE = also write the step's token into the cache.  Each workgroup
+// streams `span` tokens of one (kv head, sequence) pair.  PIPE: round r+1's block-table and K/V loads are issued
+// before round r is computed (register double buffering); otherwise one buffer and higher occupancy.
 template <int G, int NT, bool POW2, bool PIPE, bool FUSE, int W>
 __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(G >= 16 ? 1 : (PIPE || G >= 8 ? 2 : (G >= 4 ? 3 : 4)))))
     attn_decode_split_kernel(bf16_t *__restrict__ out, float *__restrict__ part_o, float *__restrict__ part_ml,
