@@ -7,19 +7,25 @@
 // writes zeros.  The host tiles each segment into hip_attn_prefill_tile() rows (tile_seq, tile_q0).
 //
 // Design (one workgroup = one query tile x one KV head x a group of its G query heads):
-//   * K and V tiles of 64 keys move HBM -> LDS with global_load_lds_dwordx4 (no register staging, no VALU
-//     work): each wave instruction fills four 256-byte key rows.  Two LDS stages: tile t+1 streams in while
-//     tile t is computed, one barrier per tile.  Rows are stored as 16 chunks of 16 bytes with the chunk index
-//     XOR-swizzled by the row (K: row & 15, V: 4*row & 15) so the fragment reads below are bank-conflict free;
+//   * K and V tiles of 64 keys move HBM -> LDS with buffer_load_dwordx4 ... lds (no register staging, no VALU
+//     work): each wave instruction fills four 256-byte key rows through a buffer descriptor whose base is the
+//     rows' cache block.  Buffer (MUBUF) rather than FLAT-encoded global_load_lds: a FLAT load that writes LDS
+//     makes the compiler wait for every LDS read in flight (lgkmcnt(0)) wherever it waits for one, which
+//     serialises the fragment reads below.  Two LDS stages: tile t+1 streams in while tile t is computed, one
+//     barrier per tile.  Rows are stored as 16 chunks of 16 bytes with the chunk index XOR-swizzled by the row
+//     (K: row & 15, V: 4*row & 15) so the fragment reads below are bank-conflict free;
 //   * each wave owns 32 query rows of one head and computes S^T = K Q^T with v_mfma_f32_32x32x16_bf16: K
-//     (ds_read_b128 from LDS) is the A operand, Q (registers, loaded once) the B operand.  In the S^T
+//     (ds_read_b128 from LDS, issued KPF MFMA pairs ahead of use) is the A operand, Q (registers, loaded once)
+//     the B operand.  In the S^T
 //     accumulator layout every lane holds 32 keys of ONE query row, so the online softmax is lane-local except
 //     one exchange between the two half-waves;
 //   * the probabilities are rounded to bf16 in registers and used directly as the B operand of O^T = V^T P^T
 //     (the MFMA's k-slots are assigned to keys in the order the S^T accumulator holds them).  The V^T A operand
 //     comes straight from the row-major V tile through ds_read_b64_tr_b16: a 16-lane group whose lane 4j+m
 //     addresses four dims of key j receives, in lane i, key j's value of dim i -- the transpose happens in the
-//     LDS read;
+//     LDS read.  The first VPF of these reads are issued before the softmax (they do not depend on P) and the
+//     rest stay VPF MFMAs ahead; scheduling barriers keep the compiler from sinking the reads back next to
+//     their uses;
 //   * online softmax in base 2 with scale * log2 e folded in, fp32 row state, lazy rescaling (the reference max
 //     moves only when a row max grows by more than 2^8); causal masking only on tiles that cross a wave's
 //     diagonal; tiles wholly above a wave's diagonal are skipped by that wave;
@@ -38,6 +44,14 @@ constexpr int BQ = 64;               // query rows per tile (the value hip_attn_
 constexpr int BK = 64;               // keys per LDS tile
 constexpr int TILE = BK * HD;        // bf16 elements of one K (or V) tile: 16 KB, rows of 256 B, no padding
 constexpr float RESCALE_LOG2 = 8.f;  // lazy-rescale threshold (log2 units)
+constexpr int KPF = 3;               // K fragment pairs read ahead of the S MFMAs
+constexpr int VPF = 4;               // V^T fragments read ahead of the PV MFMAs
+
+// DMA addressing: BLOCK = block_size is a power of two and a multiple of BK (a K/V tile lies inside one block:
+// one descriptor per tile); ROW4 = block_size % 4 == 0 (the four rows of one DMA instruction lie inside one
+// block: one descriptor per instruction); FLAT = any block size (global_load_lds with per-lane addresses).
+enum DmaMode { DMA_FLAT = 0, DMA_BLOCK = 1, DMA_ROW4 = 2 };
+constexpr unsigned BUF_WORD3 = 0x00020000u;  // raw buffer descriptor, 32-bit data format
 
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
@@ -55,9 +69,17 @@ __device__ __forceinline__ void dma16(const bf16_t *gsrc, bf16_t *ldst) {
                                      (__attribute__((address_space(3))) void *)ldst, 16, 0, 0);
 }
 
-// NW = waves per workgroup (2 per head: rows 0-31 and 32-63 of the tile); FAST = block_size is a power of two
-// and a multiple of BK (every K/V tile then lies inside one block).
-template <int NW, bool FAST>
+// 16 bytes per lane from (descriptor base + byte offset voff) into LDS at ldst (wave-uniform) + 16 * lane
+__device__ __forceinline__ void bufdma16(__amdgpu_buffer_rsrc_t rs, int voff, bf16_t *ldst) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void *)ldst, 16, voff, 0, 0, 0);
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const bf16_t *base, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, bytes, BUF_WORD3);
+}
+
+// NW = waves per workgroup (2 per head: rows 0-31 and 32-63 of the tile); MODE = DmaMode.
+template <int NW, int MODE>
 __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 2 ? 1 : 2)))
     attn_prefill_kernel(bf16_t *__restrict__ out, const bf16_t *__restrict__ q, const bf16_t *__restrict__ kc,
                         const bf16_t *__restrict__ vc, const int *__restrict__ block_tables,
@@ -124,26 +146,37 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
     auto issue = [&](int it, bf16_t *Kd, bf16_t *Vd) {
         const int kb0 = it * BK;
         const int last = kend - 1 - kb0;  // keys past kend reread the last valid key (finite data)
-        long kbase = 0;
-        if (FAST) {
+        __amdgpu_buffer_rsrc_t krs, vrs;
+        if (MODE == DMA_BLOCK) {  // the whole tile lies in one block: one descriptor pair per tile
             const int phys = bt[__builtin_amdgcn_readfirstlane(kb0 >> bs_shift)];
-            kbase = (long)phys * blk_stride + head_off + (long)(kb0 & (block_size - 1)) * HD;
+            const long kbase = (long)phys * blk_stride + head_off + (long)(kb0 & (block_size - 1)) * HD;
+            krs = make_rsrc(kc + kbase, TILE * 2);
+            vrs = make_rsrc(vc + kbase, TILE * 2);
         }
 #pragma unroll
         for (int i = 0; i < LOADS; ++i) {
             const int rbase = 4 * (wave + NW * i);
             const int r = rbase + drow;
-            const int key = min(r, last);
-            long src;
-            if (FAST) {
-                src = kbase + (long)key * HD;
+            const int kswz = (dchunk ^ (r & 15)) << 4, vswz = (dchunk ^ ((r << 2) & 15)) << 4;  // bytes
+            if (MODE == DMA_BLOCK) {
+                const int voff = min(r, last) * (HD * 2);
+                bufdma16(krs, voff + kswz, Kd + rbase * HD);
+                bufdma16(vrs, voff + vswz, Vd + rbase * HD);
+            } else if (MODE == DMA_ROW4) {
+                // rows rbase..rbase+3 (clamped to last) lie in one block: key t0 + d, d in 0..3
+                const int t0 = __builtin_amdgcn_readfirstlane(kb0 + min(rbase, last));
+                const int bi = bs_shift >= 0 ? (t0 >> bs_shift) : t0 / block_size;
+                const long base = (long)bt[bi] * blk_stride + head_off + (long)(t0 - bi * block_size) * HD;
+                const int voff = (min(r, last) - min(rbase, last)) * (HD * 2);
+                bufdma16(make_rsrc(kc + base, 4 * HD * 2), voff + kswz, Kd + rbase * HD);
+                bufdma16(make_rsrc(vc + base, 4 * HD * 2), voff + vswz, Vd + rbase * HD);
             } else {
-                const int t = kb0 + key;
+                const int t = kb0 + min(r, last);
                 const int bi = t / block_size;
-                src = (long)bt[bi] * blk_stride + head_off + (long)(t - bi * block_size) * HD;
+                const long src = (long)bt[bi] * blk_stride + head_off + (long)(t - bi * block_size) * HD;
+                dma16(kc + src + (kswz >> 1), Kd + rbase * HD);
+                dma16(vc + src + (vswz >> 1), Vd + rbase * HD);
             }
-            dma16(kc + src + ((dchunk ^ (r & 15)) << 3), Kd + rbase * HD);
-            dma16(vc + src + ((dchunk ^ ((r << 2) & 15)) << 3), Vd + rbase * HD);
         }
     };
 
@@ -182,13 +215,34 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
             for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
+        bf16x8_t ka[8], kb[8];  // K fragments of keys 0-31 and 32-63, read KPF steps ahead
+#pragma unroll
+        for (int c = 0; c < KPF; ++c) {
+            ka[c] = *reinterpret_cast<const bf16x8_t *>(Ks + koff[c]);
+            kb[c] = *reinterpret_cast<const bf16x8_t *>(Ks + koff[c] + 32 * HD);
+        }
 #pragma unroll
         for (int c = 0; c < 8; ++c) {  // two independent accumulation chains interleaved
-            const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t *>(Ks + koff[c]);
-            const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t *>(Ks + koff[c] + 32 * HD);
-            sacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qf[c], sacc[0], 0, 0, 0);
-            sacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qf[c], sacc[1], 0, 0, 0);
+            if (c + KPF < 8) {
+                ka[c + KPF] = *reinterpret_cast<const bf16x8_t *>(Ks + koff[c + KPF]);
+                kb[c + KPF] = *reinterpret_cast<const bf16x8_t *>(Ks + koff[c + KPF] + 32 * HD);
+            }
+            sacc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[c], qf[c], sacc[0], 0, 0, 0);
+            sacc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kb[c], qf[c], sacc[1], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);  // keep the read-ahead order
         }
+        // V^T fragment i = kc16 * 4 + db: keys kc16*16 + hh*4 + j (+8), dims db*32 + ...; the first VPF do not
+        // depend on P and are read before the softmax
+        bf16x8_t va[16];
+        auto vread = [&](int i) {
+            const bf16_t *vp = Vs + (i >> 2) * 16 * HD + voff[i & 3];
+            const s16x4_t lo = ds_read_tr(vp);           // keys hh*4 + j
+            const s16x4_t hi = ds_read_tr(vp + 8 * HD);  // keys 8 + hh*4 + j
+            va[i] = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        };
+#pragma unroll
+        for (int i = 0; i < VPF; ++i) vread(i);
+        __builtin_amdgcn_sched_barrier(0);
         // lane holds row my_row, keys kb0 + kb*32 + (r/4)*8 + hh*4 + r%4 (raw dot products)
         float mx = -INFINITY;
 #pragma unroll
@@ -232,15 +286,11 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
         }
         // ---- O^T[dim][row] += V^T P^T: four independent accumulators per 16-key step ----
 #pragma unroll
-        for (int kc16 = 0; kc16 < 4; ++kc16)
-#pragma unroll
-            for (int db = 0; db < 4; ++db) {
-                const bf16_t *vp = Vs + kc16 * 16 * HD + voff[db];
-                const s16x4_t lo = ds_read_tr(vp);           // keys hh*4 + j
-                const s16x4_t hi = ds_read_tr(vp + 8 * HD);  // keys 8 + hh*4 + j
-                const bf16x8_t a = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pf[kc16], o[db], 0, 0, 0);
-            }
+        for (int i = 0; i < 16; ++i) {
+            if (i + VPF < 16) vread(i + VPF);
+            o[i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[i], pf[i >> 2], o[i & 3], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
     };
     auto compute = [&](int it, const bf16_t *Ks, const bf16_t *Vs) {
         const int kb0 = it * BK;
@@ -287,19 +337,27 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
         }
 }
 
+template <int NW, int MODE>
+void launch_prefill_mode(long grid, bf16_t *out, const bf16_t *q, const bf16_t *kc, const bf16_t *vc, const int *bt,
+                         const int *ctx, const int *cu_q, const int *tile_seq, const int *tile_q0, int n_tiles, int nq,
+                         int nkv, int G, int head_groups, int max_blocks, int block_size, int bs_shift, float sl2) {
+    hipLaunchKernelGGL((attn_prefill_kernel<NW, MODE>), dim3((unsigned)grid), dim3(64 * NW), 0, g_llmgen_stream, out, q,
+                       kc, vc, bt, ctx, cu_q, tile_seq, tile_q0, n_tiles, nq, nkv, G, head_groups, max_blocks,
+                       block_size, bs_shift, sl2);
+}
+
 template <int NW>
-void launch_prefill(bool fast, int head_groups, bf16_t *out, const bf16_t *q, const bf16_t *kc, const bf16_t *vc,
+void launch_prefill(int mode, int head_groups, bf16_t *out, const bf16_t *q, const bf16_t *kc, const bf16_t *vc,
                     const int *bt, const int *ctx, const int *cu_q, const int *tile_seq, const int *tile_q0,
                     int n_tiles, int nq, int nkv, int G, int max_blocks, int block_size, int bs_shift, float sl2) {
     const long grid = (long)n_tiles * nkv * head_groups;
-    if (fast)
-        hipLaunchKernelGGL((attn_prefill_kernel<NW, true>), dim3((unsigned)grid), dim3(64 * NW), 0, g_llmgen_stream,
-                           out, q, kc, vc, bt, ctx, cu_q, tile_seq, tile_q0, n_tiles, nq, nkv, G, head_groups,
-                           max_blocks, block_size, bs_shift, sl2);
-    else
-        hipLaunchKernelGGL((attn_prefill_kernel<NW, false>), dim3((unsigned)grid), dim3(64 * NW), 0, g_llmgen_stream,
-                           out, q, kc, vc, bt, ctx, cu_q, tile_seq, tile_q0, n_tiles, nq, nkv, G, head_groups,
-                           max_blocks, block_size, bs_shift, sl2);
+    auto go = [&](auto m) {
+        launch_prefill_mode<NW, decltype(m)::value>(grid, out, q, kc, vc, bt, ctx, cu_q, tile_seq, tile_q0, n_tiles,
+                                                    nq, nkv, G, head_groups, max_blocks, block_size, bs_shift, sl2);
+    };
+    if (mode == DMA_BLOCK) go(std::integral_constant<int, DMA_BLOCK>{});
+    else if (mode == DMA_ROW4) go(std::integral_constant<int, DMA_ROW4>{});
+    else go(std::integral_constant<int, DMA_FLAT>{});
 }
 
 }  // namespace
@@ -325,7 +383,7 @@ extern "C" void hip_attn_prefill(bf16_t *out, const bf16_t *q, const bf16_t *k_c
         return;
     }
     const int bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz(block_size) : -1;
-    const bool fast = bs_shift >= 0 && block_size % BK == 0;
+    const int mode = (bs_shift >= 0 && block_size % BK == 0) ? DMA_BLOCK : (block_size % 4 == 0 ? DMA_ROW4 : DMA_FLAT);
     const float sl2 = scale * LLMGEN_LOG2E;
     // two waves per head; at most 8 waves (4 heads) per workgroup, the rest of the group in further workgroups
     const int heads_per_wg = G < 4 ? G : 4;
@@ -336,11 +394,11 @@ extern "C" void hip_attn_prefill(bf16_t *out, const bf16_t *q, const bf16_t *k_c
     llmgen_decode_rows_of_prefill(out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq, n_tiles, nq,
                                   nkv, max_blocks, block_size, scale, side);
     switch (heads_per_wg) {
-        case 1: launch_prefill<2>(fast, head_groups, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq,
+        case 1: launch_prefill<2>(mode, head_groups, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq,
                                   tile_q0, n_tiles, nq, nkv, G, max_blocks, block_size, bs_shift, sl2); break;
-        case 2: launch_prefill<4>(fast, head_groups, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq,
+        case 2: launch_prefill<4>(mode, head_groups, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq,
                                   tile_q0, n_tiles, nq, nkv, G, max_blocks, block_size, bs_shift, sl2); break;
-        default: launch_prefill<8>(fast, head_groups, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq,
+        default: launch_prefill<8>(mode, head_groups, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq,
                                    tile_q0, n_tiles, nq, nkv, G, max_blocks, block_size, bs_shift, sl2); break;
     }
     llmgen_join_side_stream(side);

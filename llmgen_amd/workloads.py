@@ -13,7 +13,8 @@ Configurations (shape Qwen3-0.6B unless stated: 16 Q heads, 8 KV heads, head_dim
   c5d decode, 32 Q / 8 KV heads (GQA 4), 16 sequences at ctx 32768, permuted blocks, std 1
   c5p prefill, 32 Q / 8 KV heads, one 16384-token causal prompt, permuted blocks, std 1
 Reference test cases (src/backend/cuda/kernel_test.zig:151-232, src/backend/cpu/attention.zig:188-251) are
-``kt_prefill``, ``kt_decode`` and ``cpu_mixed``, with U(-1, 1) inputs from a seeded generator.
+``kt_prefill``, ``kt_decode`` and ``cpu_mixed``, with U(-1, 1) inputs from a seeded generator.  Further small
+steps cover other GQA group sizes (``gqa*``) and block sizes 48 and 6 (``bs48*``, ``bs6*``).
 """
 from __future__ import annotations
 
@@ -235,6 +236,20 @@ def make(name: str, seed: Optional[int] = None) -> Workload:
         return Workload(name, 16, 4, 128, 48, nb, 24, 1152, ents, std=1.0, seed=s,
                         decode=None if name == "bs48d" else False,
                         note=f"block size 48, GQA 4 ({'decode' if name == 'bs48d' else 'mixed'})")
+    if name in ("bs6", "bs6d"):
+        # a block size that is not a multiple of 4 (the prefill kernel's per-lane DMA path), GQA 2
+        s = 43 if seed is None else seed
+        rng = np.random.default_rng(s)
+        if name == "bs6":
+            spec = [(50, 70), (0, 33), (11, 1), (0, 1)]
+        else:
+            spec = [(c - 1, 1) for c in (6, 7, 120, 1, 61)]
+        ctxs = [a + b for a, b in spec]
+        tables, nb = _tables(rng, ctxs, 6, permute=True, extra_blocks=2)
+        ents = [Entry(a, b, t) for (a, b), t in zip(spec, tables)]
+        return Workload(name, 8, 4, 128, 6, nb, 24, 144, ents, std=1.0, seed=s,
+                        decode=None if name == "bs6d" else False,
+                        note=f"block size 6, GQA 2 ({'decode' if name == 'bs6d' else 'mixed'})")
     raise KeyError(name)
 
 
