@@ -480,17 +480,6 @@ int *merge_counters() {
     return ptr[dev];
 }
 
-int num_compute_units() {
-    static int n = 0;
-    if (n == 0) {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-            n = 256;
-    }
-    return n;
-}
-
 // single-buffered rounds at 3-4 waves per SIMD measure faster than register double buffering at 2 (c2, c5d);
 // GQA groups of 8+ need the registers for o anyway
 bool use_pipe(int G) {
@@ -504,7 +493,7 @@ int decode_waves(int G, long pairs) {
     static const int forced = env_int("LLMGEN_DECODE_WAVES", 0);
     if (G > 4) return 4;
     if (forced == 4 || forced == 8) return forced;
-    return pairs * 2 >= num_compute_units() ? 8 : 4;
+    return pairs * 2 >= llmgen_num_cus() ? 8 : 4;
 }
 
 void launch_decode_rows(dim3 grid, const DecodeArgs &a, int G) {
@@ -545,7 +534,7 @@ void decode_launch(bf16_t *out, const bf16_t *q, const bf16_t *k_new, const bf16
     const long total = (long)nkv * S * max_parts;
     static const int wg_per_cu = env_int("LLMGEN_DECODE_WG_PER_CU", 2);
     const int W = decode_waves(G, (long)S * nkv);
-    const long target = (long)wg_per_cu * num_compute_units() * 4 / W;
+    const long target = (long)wg_per_cu * llmgen_num_cus() * 4 / W;
     const int k = (int)(total > target ? total / target : 1);
     const int nparts = (max_parts + k - 1) / k;
     int *counters = (long)S * nkv <= MAX_MERGE_SEGMENTS ? merge_counters() : nullptr;

@@ -90,3 +90,6 @@ __attribute__((visibility("hidden"))) void llmgen_decode_rows_of_prefill(
 // kernels of one launcher concurrently; legal inside stream capture.
 __attribute__((visibility("hidden"))) hipStream_t llmgen_fork_side_stream();
 __attribute__((visibility("hidden"))) void llmgen_join_side_stream(hipStream_t side);
+
+// Internal: compute units of the current device (256 if the query fails); cached after the first call.
+__attribute__((visibility("hidden"))) int llmgen_num_cus();

@@ -46,6 +46,17 @@ void llmgen_join_side_stream(hipStream_t side) {
     HIP_WARN(hipStreamWaitEvent(g_llmgen_stream, g_join_event, 0));
 }
 
+int llmgen_num_cus() {
+    static int n = 0;
+    if (n == 0) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+    }
+    return n;
+}
+
 extern "C" {
 
 // cuda_context.cu:13-42.  Creates the global stream on device 0.  ws_bytes is accepted for signature parity

@@ -202,10 +202,10 @@ def make(name: str, seed: Optional[int] = None) -> Workload:
         ents = [Entry(40, 30, t0), Entry(40, 1, t1)]
         return Workload(name, 4, 2, 128, 16, 24, 8, 128, ents, uniform=True, seed=s, decode=False, pad_rows=1,
                         note="cpu test: chunked tail + decode + padding row")
-    if name in ("gqa1", "gqa8", "gqa16"):
+    if name in ("gqa1", "gqa2", "gqa8", "gqa16"):
         # small mixed steps at other group sizes: chunked tail + fresh prompt + decode rows, bs 32, permuted blocks
-        s = {"gqa1": 21, "gqa8": 22, "gqa16": 23}[name] if seed is None else seed
-        nq, nkv = {"gqa1": (8, 8), "gqa8": (16, 2), "gqa16": (32, 2)}[name]
+        s = {"gqa1": 21, "gqa2": 24, "gqa8": 22, "gqa16": 23}[name] if seed is None else seed
+        nq, nkv = {"gqa1": (8, 8), "gqa2": (8, 4), "gqa8": (16, 2), "gqa16": (32, 2)}[name]
         rng = np.random.default_rng(s)
         spec = [(200, 90), (0, 150), (333, 1), (64, 1), (0, 1)]
         ctxs = [a + b for a, b in spec]

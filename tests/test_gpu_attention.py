@@ -35,7 +35,7 @@ def _sample_rows(wl, meta, n_random=48, seed=0):
 
 
 @pytest.mark.parametrize("name", ["kt_prefill", "cpu_mixed", "c1", "c2", "gqa1", "gqa8", "gqa16",
-                                  "gqa1d", "gqa8d", "gqa16d", "bs48", "bs48d", "bs6", "bs6d"])
+                                  "gqa1d", "gqa8d", "gqa16d", "bs48", "bs48d", "bs6", "bs6d", "gqa2"])
 def test_step_matches_oracle_all_rows(gpu, name):
     wl = make(name)
     print(f"[gpu-test] {name}", flush=True)
@@ -317,3 +317,4 @@ def test_zero_sized_launches_are_noops(gpu):
     torch.cuda.synchronize()
     check_hip_error("zero-sized launches")
     np.testing.assert_array_equal(to_u16(out), before)
+
