@@ -104,9 +104,10 @@ class Step:
                                    wl.max_blocks, wl.block_size, g.attn_scale, g.part_o, g.part_ml,
                                    S.part_size(g.n_seq), S.max_parts(g.n_seq, wl.max_model_len))
         else:
-            self.L.hip_attn_prefill(self.out.data_ptr(), self.t["q"].data_ptr(), self.layer.k.data_ptr(),
-                                    self.layer.v.data_ptr(), g.block_tables, g.ctx, g.cu_q, g.tile_seq, g.tile_q0,
-                                    g.n_tiles, wl.nq, wl.nkv, wl.hd, wl.max_blocks, wl.block_size, g.attn_scale)
+            self.L.hip_attn_prefill_rows(self.out.data_ptr(), self.t["q"].data_ptr(), self.layer.k.data_ptr(),
+                                         self.layer.v.data_ptr(), g.block_tables, g.ctx, g.cu_q, g.tile_seq,
+                                         g.tile_q0, g.n_tiles, wl.nq, wl.nkv, wl.hd, wl.max_blocks, wl.block_size,
+                                         g.attn_scale, g.single_rows)
 
     def full_step(self):
         self.A.PagedAttentionImpl.execute(0, self.node)

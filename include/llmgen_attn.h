@@ -72,6 +72,16 @@ void hip_attn_prefill(uint16_t *out, const uint16_t *q, const uint16_t *k_cache,
                       const int32_t *tile_seq, const int32_t *tile_q0, int n_tiles, int nq, int nkv, int hd,
                       int max_blocks, int block_size, float scale);
 
+/* hip_attn_prefill for a caller that knows how many segments of the step have one query row (the decode rows of
+ * a mixed step, and padding rows): single_rows == 0 skips the launch that serves such rows, > 0 runs it, < 0
+ * means unknown and behaves as hip_attn_prefill.  No reference counterpart (the reference kernel runs decode rows
+ * as one-row prefill tiles); the executor slice (llmgen_paged_attention) passes the count it has from its
+ * entries, so a pure prefill step does not pay for a grid of workgroups that find nothing to do. */
+void hip_attn_prefill_rows(uint16_t *out, const uint16_t *q, const uint16_t *k_cache, const uint16_t *v_cache,
+                           const int32_t *block_tables, const int32_t *ctx_lens, const int32_t *cu_q,
+                           const int32_t *tile_seq, const int32_t *tile_q0, int n_tiles, int nq, int nkv, int hd,
+                           int max_blocks, int block_size, float scale, int single_rows);
+
 /* Replaces cuda_attn_prefill_tile (attention_v1.zig:48): query rows per prefill tile (64). */
 int hip_attn_prefill_tile(void);
 

@@ -58,6 +58,9 @@ typedef struct llmgen_step_state {
     size_t max_model_len;
     void *seed, *pos, *slots, *cu_q, *ctx, *last, *temps, *tile_seq, *tile_q0, *block_tables;
     void *cos_sin, *part_o, *part_ml, *sample_scratch;
+    int32_t single_rows; /* segments with one query row (decode / padding rows); -1 = unknown.  Not in the
+                            reference's StepState: bind_step sets -1, the caller sets the count it knows
+                            (llmgen_single_rows) and llmgen_paged_attention passes it to hip_attn_prefill_rows. */
 } llmgen_step_state;
 
 llmgen_layout llmgen_layout_init(size_t n_tok, size_t n_seq, size_t n_tiles, size_t max_blocks);
@@ -68,6 +71,8 @@ int llmgen_entry_emits(const llmgen_seq *seqs, const llmgen_entry *e);
 /* executor.zig:530-552: decode step iff every entry has q_len == 1 and emits; prefill tiles per entry. */
 int llmgen_step_is_decode(const llmgen_seq *seqs, const llmgen_entry *entries, int n_entries);
 int llmgen_step_tiles(const llmgen_entry *entries, int n_entries, int pf_tile);
+/* Segments of the step with one query row: entries with q_len == 1 plus the seq_num - n_entries padding rows. */
+int llmgen_single_rows(const llmgen_entry *entries, int n_entries, int seq_num);
 
 /* executor.zig:772-861.  Writes the step into meta_host (lay.total bytes).  seq_num >= n_entries adds padding
  * rows (id 0, pos 0, slot -1, ctx 0, temperature 0, zero block-table row).  *step_seed advances by the

@@ -63,6 +63,7 @@ class StepState:
     block_tables: int = 0
     part_o: int = 0
     part_ml: int = 0
+    single_rows: int = -1  # segments with one query row (-1 unknown); not in the reference's StepState
 
 
 g_step = StepState()
@@ -154,9 +155,9 @@ class PagedAttentionImpl:
                               s.part_o, s.part_ml, stepmod.part_size(s.n_seq),
                               stepmod.max_parts(s.n_seq, s.max_model_len))
         else:
-            L.hip_attn_prefill(_ptr(out.data), _ptr(q), _ptr(kv.k), _ptr(kv.v), s.block_tables, s.ctx, s.cu_q,
-                               s.tile_seq, s.tile_q0, s.n_tiles, s.n_head, s.n_kv_head, s.head_dim, s.max_blocks,
-                               s.block_size, s.attn_scale)
+            L.hip_attn_prefill_rows(_ptr(out.data), _ptr(q), _ptr(kv.k), _ptr(kv.v), s.block_tables, s.ctx,
+                                    s.cu_q, s.tile_seq, s.tile_q0, s.n_tiles, s.n_head, s.n_kv_head, s.head_dim,
+                                    s.max_blocks, s.block_size, s.attn_scale, s.single_rows)
 
 
 # attention_v1.zig:123: the legacy FLASH_ATTN node runs the same implementation
@@ -200,6 +201,7 @@ def bind_step(meta: "stepmod.StepMeta", ws: Workspace, nq: int, nkv: int, hd: in
     for name in ("pos", "slots", "cu_q", "ctx", "last", "tile_seq", "tile_q0", "block_tables"):
         setattr(g, name, base + 4 * off[name])
     g.part_o, g.part_ml = ws.part_o.data_ptr(), ws.part_ml.data_ptr()
+    g.single_rows = meta.single_rows()
     return g
 
 

@@ -71,6 +71,12 @@ int llmgen_step_tiles(const llmgen_entry *entries, int n_entries, int pf_tile) {
     return n;
 }
 
+int llmgen_single_rows(const llmgen_entry *entries, int n_entries, int seq_num) {
+    int n = seq_num > n_entries ? seq_num - n_entries : 0;
+    for (int i = 0; i < n_entries; ++i) n += entries[i].q_len == 1;
+    return n;
+}
+
 int llmgen_fill_meta(uint8_t *meta_host, llmgen_layout lay, const llmgen_seq *seqs, const llmgen_entry *entries,
                      int n_entries, int seq_num, int n_tiles, int pf_tile, int block_size, int max_blocks,
                      uint64_t *step_seed) {
@@ -164,6 +170,7 @@ void llmgen_bind_step(llmgen_step_state *st, void *meta_dev, llmgen_layout lay, 
     st->part_o = part_o;
     st->part_ml = part_ml;
     st->sample_scratch = sample_scratch;
+    st->single_rows = -1;
 }
 
 int llmgen_part_size(int n_seq) {
@@ -202,10 +209,10 @@ int llmgen_paged_attention(const llmgen_step_state *st, uint16_t *out, const uin
         if (!k || !v) return -1;
         hip_store_kv(k, v, slots, k_cache, v_cache, st->n_tok, st->n_kv_head, st->head_dim, st->block_size);
     }
-    hip_attn_prefill(out, q, k_cache, v_cache, bt, ctx, static_cast<const int32_t *>(st->cu_q),
-                     static_cast<const int32_t *>(st->tile_seq), static_cast<const int32_t *>(st->tile_q0),
-                     st->n_tiles, st->n_head, st->n_kv_head, st->head_dim, st->max_blocks, st->block_size,
-                     st->attn_scale);
+    hip_attn_prefill_rows(out, q, k_cache, v_cache, bt, ctx, static_cast<const int32_t *>(st->cu_q),
+                          static_cast<const int32_t *>(st->tile_seq), static_cast<const int32_t *>(st->tile_q0),
+                          st->n_tiles, st->n_head, st->n_kv_head, st->head_dim, st->max_blocks, st->block_size,
+                          st->attn_scale, st->single_rows);
     return 0;
 }
 

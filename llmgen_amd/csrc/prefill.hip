@@ -364,10 +364,11 @@ void launch_prefill(int mode, int head_groups, bf16_t *out, const bf16_t *q, con
 
 extern "C" int hip_attn_prefill_tile(void) { return BQ; }
 
-extern "C" void hip_attn_prefill(bf16_t *out, const bf16_t *q, const bf16_t *k_cache, const bf16_t *v_cache,
-                                 const int *block_tables, const int *ctx_lens, const int *cu_q, const int *tile_seq,
-                                 const int *tile_q0, int n_tiles, int nq, int nkv, int hd, int max_blocks,
-                                 int block_size, float scale) {
+extern "C" void hip_attn_prefill_rows(bf16_t *out, const bf16_t *q, const bf16_t *k_cache,
+                                      const bf16_t *v_cache, const int *block_tables, const int *ctx_lens,
+                                      const int *cu_q, const int *tile_seq, const int *tile_q0, int n_tiles, int nq,
+                                      int nkv, int hd, int max_blocks, int block_size, float scale,
+                                      int single_rows) {
     if (n_tiles <= 0) return;
     if (hd != HD) {
         fprintf(stderr, "[llmgen-hip] attn_prefill: only head_dim=128 is supported (got %d)\n", hd);
@@ -389,10 +390,15 @@ extern "C" void hip_attn_prefill(bf16_t *out, const bf16_t *q, const bf16_t *k_c
     const int heads_per_wg = G < 4 ? G : 4;
     const int head_groups = G / heads_per_wg;
     // Decode rows (q_len == 1) go to the bandwidth-oriented decode kernel on the side stream, concurrently with
-    // the MFMA kernel (which skips them) on the launch stream: HBM-bound and MFMA-bound work overlap.
-    hipStream_t side = llmgen_fork_side_stream();
-    llmgen_decode_rows_of_prefill(out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq, n_tiles, nq,
-                                  nkv, max_blocks, block_size, scale, side);
+    // the MFMA kernel (which skips them) on the launch stream: HBM-bound and MFMA-bound work overlap.  Its grid
+    // covers every tile (which tiles are single rows is device data), so it is skipped when the caller knows
+    // there are none: idle workgroups still take dispatch slots from the prefill kernel.
+    hipStream_t side = g_llmgen_stream;
+    if (single_rows != 0) {
+        side = llmgen_fork_side_stream();
+        llmgen_decode_rows_of_prefill(out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq, n_tiles, nq,
+                                      nkv, max_blocks, block_size, scale, side);
+    }
     switch (heads_per_wg) {
         case 1: launch_prefill<2>(mode, head_groups, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq,
                                   tile_q0, n_tiles, nq, nkv, G, max_blocks, block_size, bs_shift, sl2); break;
@@ -402,4 +408,12 @@ extern "C" void hip_attn_prefill(bf16_t *out, const bf16_t *q, const bf16_t *k_c
                                    tile_q0, n_tiles, nq, nkv, G, max_blocks, block_size, bs_shift, sl2); break;
     }
     llmgen_join_side_stream(side);
+}
+
+extern "C" void hip_attn_prefill(bf16_t *out, const bf16_t *q, const bf16_t *k_cache, const bf16_t *v_cache,
+                                 const int *block_tables, const int *ctx_lens, const int *cu_q, const int *tile_seq,
+                                 const int *tile_q0, int n_tiles, int nq, int nkv, int hd, int max_blocks,
+                                 int block_size, float scale) {
+    hip_attn_prefill_rows(out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq, tile_q0, n_tiles, nq, nkv,
+                          hd, max_blocks, block_size, scale, -1);
 }

@@ -50,7 +50,8 @@ class StepState(ctypes.Structure):
                 + [("attn_scale", ctypes.c_float), ("block_size", _i32), ("max_blocks", _i32),
                    ("max_model_len", _sz)]
                 + [(n, _P) for n in ("seed", "pos", "slots", "cu_q", "ctx", "last", "temps", "tile_seq", "tile_q0",
-                                     "block_tables", "cos_sin", "part_o", "part_ml", "sample_scratch")])
+                                     "block_tables", "cos_sin", "part_o", "part_ml", "sample_scratch")]
+                + [("single_rows", _i32)])
 
 
 HOST_SIGNATURES = {
@@ -58,6 +59,7 @@ HOST_SIGNATURES = {
     "llmgen_entry_emits": (ctypes.c_int, [ctypes.POINTER(Seq), ctypes.POINTER(Entry)]),
     "llmgen_step_is_decode": (ctypes.c_int, [ctypes.POINTER(Seq), ctypes.POINTER(Entry), ctypes.c_int]),
     "llmgen_step_tiles": (ctypes.c_int, [ctypes.POINTER(Entry), ctypes.c_int, ctypes.c_int]),
+    "llmgen_single_rows": (ctypes.c_int, [ctypes.POINTER(Entry), ctypes.c_int, ctypes.c_int]),
     "llmgen_fill_meta": (ctypes.c_int, [_P, Layout, ctypes.POINTER(Seq), ctypes.POINTER(Entry), ctypes.c_int,
                                         ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                         ctypes.POINTER(ctypes.c_uint64)]),
@@ -142,6 +144,11 @@ def fill_meta(seqs: Sequence[Sequence_], entries, seq_num: int, n_tiles: int, pf
     if rc != 0:
         raise ValueError(f"llmgen_fill_meta rejected the step (rc={rc})")
     return buf, lay, seed.value
+
+
+def single_rows(entries, seq_num: int) -> int:
+    """Segments of the step with one query row (entries with q_len == 1, plus padding rows)."""
+    return L().llmgen_single_rows(_entries(entries), len(entries), seq_num)
 
 
 def segments(buf: np.ndarray, lay: Layout, n_tok: int, n_seq: int, n_tiles: int, max_blocks: int) -> dict:

@@ -209,6 +209,7 @@ class Qwen3:
         g = Hx.bind_step(self.meta_dev.data_ptr(), lay, T, S, n_tiles, decode, cfg.n_head, cfg.n_kv_head,
                          cfg.head_dim, cfg.block_size, self.max_blocks, cfg.max_model_len, self.part_o.data_ptr(),
                          self.part_ml.data_ptr(), self.sample_scratch.data_ptr(), hidden=cfg.hidden)
+        g.single_rows = Hx.single_rows(ents, S)
         d = self.device
         ids_ptr = self.meta_dev.data_ptr() + lay.ids
         H, nq, nkv, hd, F = cfg.hidden, cfg.n_head, cfg.n_kv_head, cfg.head_dim, cfg.ffn

@@ -85,6 +85,10 @@ class StepMeta:
     pos: Optional[np.ndarray] = None  # [n_tok] position of each token in its sequence (padding rows: 0)
     offsets: dict = field(default_factory=dict)
 
+    def single_rows(self) -> int:
+        """Segments with one query row (decode rows of a mixed step, padding rows)."""
+        return int(np.count_nonzero(np.diff(self.cu_q[:self.n_seq + 1]) == 1))
+
     def packed(self) -> np.ndarray:
         """One contiguous int32 buffer in Layout order (executor.zig:139-202, without ids/temps/seed, which
         attention does not read); offsets (in int32 elements) are recorded in ``self.offsets``."""

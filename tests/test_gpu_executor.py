@@ -44,6 +44,7 @@ def _run_cpp(wl, t, seqs, entries, pf_tile, seq_num=None, max_blocks=None):
     pml = torch.empty(ws["part_ml"] // 4 + 1, dtype=torch.float32, device=dev)
     st = H.bind_step(meta_dev.data_ptr(), lay, n_tok, seq_num, n_tiles, decode, wl.nq, wl.nkv, wl.hd,
                      wl.block_size, mb, wl.max_model_len, po.data_ptr(), pml.data_ptr())
+    st.single_rows = H.single_rows(entries, seq_num)
     kc, vc = t["kc"].clone(), t["vc"].clone()
 
     def rows(x):

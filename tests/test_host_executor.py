@@ -101,3 +101,20 @@ def test_buckets_and_workspace_match_python():
     assert (w["part_o"], w["part_ml"]) == (po, pml)
     assert w["meta"] == H.layout(2048, 32, 2048 // 64 + 32, 4096 // 16).total
     assert H.L().llmgen_part_size(16) == S.part_size(16) and H.L().llmgen_max_parts(5, 1000) == S.max_parts(5, 1000)
+
+
+def test_single_rows_counts_one_row_segments():
+    """llmgen_single_rows (the count hip_attn_prefill_rows takes) equals the one-row segments of the packed
+    cu_q, for a mixed step and for a padded decode bucket."""
+    seqs, entries = _mixed()
+    tile, bs, mb = 64, 16, 10
+    n_tiles = sum((e[2] + tile - 1) // tile for e in entries)
+    buf, lay, _ = H.fill_meta(seqs, entries, len(entries), n_tiles, tile, bs, mb)
+    seg = H.segments(buf, lay, sum(e[2] for e in entries), len(entries), n_tiles, mb)
+    expect = int(np.count_nonzero(np.diff(seg["cu_q"]) == 1))
+    assert H.single_rows(entries, len(entries)) == expect
+    py = S.fill_meta([S.Entry(e[1], e[2], seqs[e[0]].block_table) for e in entries], bs, mb, tile, decode=False)
+    assert py.single_rows() == expect
+    # padding rows of a bucket are one-row segments too
+    assert H.single_rows([(0, 99, 1), (1, 10, 1)], 4) == 4
+    assert H.single_rows([(0, 0, 70)], 1) == 0
