@@ -318,3 +318,34 @@ def test_zero_sized_launches_are_noops(gpu):
     check_hip_error("zero-sized launches")
     np.testing.assert_array_equal(to_u16(out), before)
 
+
+
+@pytest.mark.parametrize("name", ["cpu_mixed", "bs48", "bs6", "gqa8", "c4", "c3"])
+def test_prefill_rows_hint_matches_unknown_count(gpu, name):
+    """hip_attn_prefill_rows with the step's single-row segment count (0 for c3: no decode-row launch) gives the
+    bit-identical output of hip_attn_prefill (count unknown)."""
+    wl = make(name)
+    print(f"[gpu-test] {name}", flush=True)
+    t = wl.tensors(device="cuda")
+    meta = wl.meta(lib().hip_attn_prefill_tile())
+    assert not meta.decode
+    L = lib()
+    kc, vc = t["kc"].clone(), t["vc"].clone()
+    seg = torch.from_numpy(meta.packed()).to("cuda")
+    off = {k: seg.data_ptr() + 4 * v for k, v in meta.offsets.items()}
+    L.hip_store_kv(t["k"].data_ptr(), t["v"].data_ptr(), off["slots"], kc.data_ptr(), vc.data_ptr(), wl.n_tok,
+                   wl.nkv, wl.hd, wl.block_size)
+    outs = []
+    for hint in (None, meta.single_rows()):
+        out = torch.full((wl.n_tok, wl.nq, wl.hd), float("nan"), dtype=torch.bfloat16, device="cuda")
+        args = (out.data_ptr(), t["q"].data_ptr(), kc.data_ptr(), vc.data_ptr(), off["block_tables"], off["ctx"],
+                off["cu_q"], off["tile_seq"], off["tile_q0"], meta.n_tiles, wl.nq, wl.nkv, wl.hd, wl.max_blocks,
+                wl.block_size, wl.scale)
+        if hint is None:
+            L.hip_attn_prefill(*args)
+        else:
+            L.hip_attn_prefill_rows(*args, hint)
+        torch.cuda.synchronize()
+        check_hip_error(name)
+        outs.append(to_u16(out))
+    np.testing.assert_array_equal(outs[1], outs[0])
