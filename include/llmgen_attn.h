@@ -6,7 +6,7 @@
  *   - the three attention launchers: src/backend/cuda/attention/attention_v1.zig:10-48
  *   - the device context:            src/backend/cuda/cuda_context.zig:1-11, cuda_context.cu:13-126
  *   - device memory helpers:         src/backend/cuda/memory/memory.zig:1-11
- * A host that binds `cuda_X` today binds `hip_X` here (see INTEGRATION.md for the Zig stubs).
+ * A host that binds `cuda_X` today binds `hip_X` here, with the same argument list.
  *
  * Conventions (same as the reference):
  *   - bf16 tensors are passed as uint16_t bit patterns; index tensors are int32; all pointers are device
