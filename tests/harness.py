@@ -10,7 +10,7 @@ from llmgen_amd import attention as A
 from llmgen_amd._lib import lib
 from llmgen_amd.workloads import Workload, to_u16
 
-MAX_ABS = 2e-2  # north-star bf16 tolerance against the f32 result before rounding
+MAX_ABS = 2e-2  # bf16 output tolerance against the f32 result before rounding (with REL_L2)
 REL_L2 = 1e-2
 
 

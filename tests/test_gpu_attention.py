@@ -1,7 +1,7 @@
 """GPU parity: the HIP path (through the C-ABI) against the CPU oracle on the same seeded inputs.
 
 Bars: store_kv bit-exact; attention within max-abs 2e-2 and rel-L2 1e-2 of the oracle's f32 result before bf16
-rounding (the north-star tolerance), and padding rows exactly 0.
+rounding, and padding rows exactly 0.
 """
 from __future__ import annotations
 
