@@ -26,8 +26,10 @@
 //     LDS read.  The first VPF of these reads are issued before the softmax (they do not depend on P) and the
 //     rest stay VPF MFMAs ahead; scheduling barriers keep the compiler from sinking the reads back next to
 //     their uses;
-//   * online softmax in base 2 with scale * log2 e folded in, fp32 row state, lazy rescaling (the reference max
-//     moves only when a row max grows by more than 2^8); causal masking only on tiles that cross a wave's
+//   * online softmax in base 2 with scale * log2 e folded in and fp32 row state.  The first tile sets each row's
+//     reference from its row max; later tiles take their probabilities against that reference without a row
+//     max (a VALU chain and a half-wave exchange per tile saved) and move it only when a tile's row sum passes
+//     2^64, recomputing that tile against its row max.  Causal masking only on tiles that cross a wave's
 //     diagonal; tiles wholly above a wave's diagonal are skipped by that wave;
 //   * grid is 1-D with the KV head fastest, so every workgroup of one KV head lands on the same XCD (8 XCDs,
 //     round-robin dispatch) and its K/V tiles stay in that XCD's L2; later query tiles go first.
@@ -43,7 +45,7 @@ constexpr int HD = 128;
 constexpr int BQ = 64;               // query rows per tile (the value hip_attn_prefill_tile returns)
 constexpr int BK = 64;               // keys per LDS tile
 constexpr int TILE = BK * HD;        // bf16 elements of one K (or V) tile: 16 KB, rows of 256 B, no padding
-constexpr float RESCALE_LOG2 = 8.f;  // lazy-rescale threshold (log2 units)
+constexpr float RESCALE_LOG2 = 8.f;  // lazy-rescale threshold (log2 units) of the tiles that take a row max
 constexpr int KPF = 3;               // K fragment pairs read ahead of the S MFMAs
 constexpr int VPF = 4;               // V^T fragments read ahead of the PV MFMAs
 
@@ -244,37 +246,64 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
         for (int i = 0; i < VPF; ++i) vread(i);
         __builtin_amdgcn_sched_barrier(0);
         // lane holds row my_row, keys kb0 + kb*32 + (r/4)*8 + hh*4 + r%4 (raw dot products)
-        float mx = -INFINITY;
+        if (MASK) {
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+            for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                if (MASK) {
+                for (int r = 0; r < 16; ++r) {
                     const int key = kb0 + kb * 32 + (r >> 2) * 8 + hh * 4 + (r & 3);
                     if (!row_valid || key > my_pos) sacc[kb][r] = -INFINITY;
                 }
-                mx = fmaxf(mx, sacc[kb][r]);
-            }
-        mx = fmaxf(mx, lane_xor(mx, 32)) * scale_log2;  // scale > 0 commutes with max
-        const bool grow = mx > m_run + RESCALE_LOG2;
-        const float m_new = grow ? mx : m_run;
-        const float m_use = (MASK && m_new == -INFINITY) ? 0.f : m_new;
-        const float corr = grow ? fast_exp2(m_run - m_use) : 1.f;
-        float lsum = 0.f;
+        }
+        auto row_max = [&]() {
+            float mx = -INFINITY;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[kb][r]);
+            return fmaxf(mx, lane_xor(mx, 32)) * scale_log2;  // scale > 0 commutes with max
+        };
+        float lsum;
         bf16x8_t pf[4];  // B fragments for the four 16-key steps of P V
+        auto probs = [&](float m_use) {
+            lsum = 0.f;
 #pragma unroll
-        for (int kc16 = 0; kc16 < 4; ++kc16) {
-            const int kb = kc16 >> 1, half = kc16 & 1;
-            float p[8];
+            for (int kc16 = 0; kc16 < 4; ++kc16) {
+                const int kb = kc16 >> 1, half = kc16 & 1;
+                float p[8];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                p[e] = fast_exp2(__builtin_fmaf(sacc[kb][half * 8 + e], scale_log2, -m_use));
-                lsum += p[e];
+                for (int e = 0; e < 8; ++e) {
+                    p[e] = fast_exp2(__builtin_fmaf(sacc[kb][half * 8 + e], scale_log2, -m_use));
+                    lsum += p[e];
+                }
+                u32x4_t w;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) w[e] = pack_bf16x2(p[2 * e], p[2 * e + 1]);
+                pf[kc16] = __builtin_bit_cast(bf16x8_t, w);
             }
-            u32x4_t w;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) w[e] = pack_bf16x2(p[2 * e], p[2 * e + 1]);
-            pf[kc16] = __builtin_bit_cast(bf16x8_t, w);
+        };
+        // Once every row of the wave has a finite reference m_run, the tile's probabilities are taken against
+        // it without a row max: they may exceed 1 (f32 and bf16 share the exponent range, and o / l is
+        // unchanged by the common factor).  Only a row sum beyond 2^64 (scores far above the reference) moves
+        // the reference, recomputing the tile against the new row max.
+        bool grow = false;
+        float m_new = m_run, corr = 1.f;
+        if (!__all(m_run > -INFINITY)) {
+            const float mx = row_max();
+            grow = mx > m_run + RESCALE_LOG2;
+            m_new = grow ? mx : m_run;
+            const float m_use = m_new == -INFINITY ? 0.f : m_new;
+            corr = grow ? fast_exp2(m_run - m_use) : 1.f;
+            probs(m_use);
+        } else {
+            probs(m_run);
+            if (__any(!(lsum <= 0x1p64f))) {
+                const float mx = row_max();
+                grow = mx > m_run;
+                m_new = grow ? mx : m_run;
+                corr = grow ? fast_exp2(m_run - m_new) : 1.f;
+                probs(m_new);
+            }
         }
         l_run = l_run * corr + lsum;
         m_run = m_new;

@@ -380,3 +380,30 @@ def test_uniform_scores_give_mean_v(gpu, name):
         want = mean[ctx - q_len:ctx]  # [q_len, nkv, hd]
         want = np.repeat(want, G, axis=1)  # heads kvh*G .. kvh*G+G-1 share kv head kvh
         np.testing.assert_allclose(got[b:e], want, rtol=8e-3, atol=2e-3, err_msg=f"{name} sequence {s}")
+
+
+@pytest.mark.parametrize("name", ["kt_prefill", "kt_decode", "gqa8"])
+def test_scores_growing_along_the_keys(gpu, name):
+    """Scores that grow by ~1.6 (log2 units) per key, to ~245 at the last key: every later key tile exceeds the
+    running softmax reference by far more than 2^64, so the kernels must move their reference (and rescale the
+    accumulated output) again and again.  q = 1, key at position p = 0.1 p in every dim, both in the cache
+    history and in this step's k."""
+    wl = make(name)
+    print(f"[gpu-test] {name}", flush=True)
+    t = wl.tensors(device="cpu")
+    meta = wl.meta(lib().hip_attn_prefill_tile())
+    t["q"] = torch.ones_like(t["q"])
+    kc, k = t["kc"].float(), t["k"].float()
+    for s in range(meta.n_seq):
+        b, e, ctx = int(meta.cu_q[s]), int(meta.cu_q[s + 1]), int(meta.ctx[s])
+        for p in range(ctx):
+            val = 0.1 * p
+            if p < ctx - (e - b):  # history: in the cache at the block table's slot
+                kc[meta.block_tables[s][p // wl.block_size], :, p % wl.block_size, :] = val
+            else:
+                k[b + p - (ctx - (e - b))] = val
+    t["kc"], t["k"] = kc.to(torch.bfloat16), k.to(torch.bfloat16)
+    td = {n: x.to("cuda") for n, x in t.items()}
+    out, _, _ = run_gpu(wl, td)
+    _, _, _, of = run_oracle(wl, t)
+    compare(to_u16(out), of, f"{name} growing scores")
