@@ -112,10 +112,10 @@ void hip_device_info(int dev, char *name, int name_cap, size_t *total_mem, int *
 }
 
 void hip_mem_info(size_t *free_mem, size_t *total_mem) {
-    if (hipMemGetInfo(free_mem, total_mem) != hipSuccess) {
-        *free_mem = 0;
-        *total_mem = 0;
-    }
+    size_t f = 0, t = 0;
+    if (hipMemGetInfo(&f, &t) != hipSuccess) f = t = 0;
+    if (free_mem) *free_mem = f;
+    if (total_mem) *total_mem = t;
 }
 
 // memory.zig:1-11
