@@ -124,6 +124,23 @@ int llmgen_fill_meta(uint8_t *meta_host, llmgen_layout lay, const llmgen_seq *se
             }
         }
     }
+    // Tiles lightest first, by the keys a tile needs (stable: entry order among equals).  The reference lists them
+    // in entry order; the prefill kernel accepts any order and dispatches the list from its end, so this makes
+    // its dispatch heaviest first across sequences (a long prompt's last tiles start before short prompts).
+    if (tile > 1) {
+        std::vector<int> order(tile);
+        std::vector<int32_t> kend(tile), s0(tseq, tseq + tile), q00(tq0, tq0 + tile);
+        for (int i = 0; i < tile; ++i) {
+            const int si = s0[i], q_len = cu_q[si + 1] - cu_q[si];
+            kend[i] = ctx[si] - q_len + std::min(q00[i] + pf_tile, q_len);
+            order[i] = i;
+        }
+        std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return kend[a] < kend[b]; });
+        for (int i = 0; i < tile; ++i) {
+            tseq[i] = s0[order[i]];
+            tq0[i] = q00[order[i]];
+        }
+    }
     // graph-bucket padding rows: ctx 0 (attention writes zeros), slot -1 (no KV write)
     for (int s = n_entries; s < seq_num; ++s) {
         if (t >= n_tok_cap) return -4;

@@ -108,7 +108,8 @@ class StepMeta:
 
 def fill_meta(entries: Sequence[Entry], block_size: int, max_blocks: int, pf_tile: int,
               seq_num: Optional[int] = None, decode: Optional[bool] = None) -> StepMeta:
-    """executor.zig:530-552 + 772-861.
+    """executor.zig:530-552 + 772-861, except that prefill tiles are listed lightest first (stable) rather than in
+    entry order, so that the kernel's last-first dispatch is heaviest first.
 
     ``decode`` defaults to the engine's rule (every entry has q_len == 1 and emits).  ``seq_num`` >= len(entries)
     adds padding rows (one token each, ctx = 0, slot = -1, zero block-table row) as for a graph bucket.  Prefill
@@ -163,5 +164,11 @@ def fill_meta(entries: Sequence[Entry], block_size: int, max_blocks: int, pf_til
         cu_q[si + 1] = t
         ctx[si] = 0
         last[si] = t - 1
+    if n_tiles > 1:
+        # lightest first by the keys a tile needs (stable); the kernel dispatches the list from its end
+        q_lens = np.diff(cu_q)[tile_seq]
+        kend = ctx[tile_seq] - q_lens + np.minimum(tile_q0 + pf_tile, q_lens)
+        order = np.argsort(kend, kind="stable")
+        tile_seq, tile_q0 = tile_seq[order].copy(), tile_q0[order].copy()
     return StepMeta(n_tok=n_tok, n_seq=n_seq, n_tiles=n_tiles, decode=decode, slots=slots, cu_q=cu_q, ctx=ctx,
                     last=last, tile_seq=tile_seq, tile_q0=tile_q0, block_tables=bt, pos=posv)

@@ -60,8 +60,9 @@ def test_fill_meta_prefill_and_padding():
         assert m.slots[j] == S.slot_of(ents[0].block_table, j, 16)
     assert m.slots[70] == 7 * 16 + 40 % 16  # position 40 lies in logical block 2 -> physical 7
     assert m.slots[71] == -1  # padding row never writes KV
-    # tiles: 70 rows -> 2 tiles, decode entry -> 1, padding -> 1
-    assert list(m.tile_seq) == [0, 0, 1, 2] and list(m.tile_q0) == [0, 64, 0, 0]
+    # tiles: 70 rows -> 2 tiles, decode entry -> 1, padding -> 1; listed lightest first by the keys each needs
+    # (padding 0, decode row 41, rows 0-63 of entry 0: 64, rows 64-69: 70)
+    assert list(m.tile_seq) == [2, 1, 0, 0] and list(m.tile_q0) == [0, 0, 0, 64]
     assert list(m.block_tables[0]) == [3, 1, 4, 0, 2, 0] and not m.block_tables[2].any()
 
 
