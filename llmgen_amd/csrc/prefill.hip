@@ -33,20 +33,11 @@
 //     diagonal; tiles wholly above a wave's diagonal are skipped by that wave;
 //   * grid is 1-D with the KV head fastest, so every workgroup of one KV head lands on the same XCD (8 XCDs,
 //     round-robin dispatch) and its K/V tiles stay in that XCD's L2; later tiles of the list go first (the
-//     executor lists tiles lightest first, so dispatch is heaviest first);
-//   * key split: a launch with few workgroups per CU slot ends on its heaviest tiles (a long prompt beside short
-//     ones).  The grid then starts with one extra workgroup for each unit (tile, head group, KV head) of the
-//     n_split / (nkv * head_groups) heaviest tiles; such a unit, when it has more key tiles than a CU slot's
-//     share of the launch, gives each of its two workgroups half of its keys.  The first of the two to finish publishes its unnormalised (o, m, l) to a
-//     library-owned scratch array and raises a ready flag; the second waits for the flag, merges the partial
-//     into its registers with the log-sum-exp rule and writes the output.  Lighter units run whole; their extra
-//     workgroup exits at once.
+//     executor lists tiles lightest first, so dispatch is heaviest first across sequences).
 #include "hip_common.h"
 
 #include <math.h>
-#include <stdlib.h>
 
-#include <algorithm>
 #include <type_traits>
 
 namespace {
@@ -64,18 +55,6 @@ constexpr int VPF = 4;               // V^T fragments read ahead of the PV MFMAs
 // block: one descriptor per instruction); FLAT = any block size (global_load_lds with per-lane addresses).
 enum DmaMode { DMA_FLAT = 0, DMA_BLOCK = 1, DMA_ROW4 = 2 };
 constexpr unsigned BUF_WORD3 = 0x00020000u;  // raw buffer descriptor, 32-bit data format
-
-// Key-split scratch: one partial per wave of a split unit (o: 64 floats per lane, then m, l; lane-minor), and an
-// arrival counter and a ready flag per unit.  The merging workgroup resets both sync words, so they are zero
-// between launches (and graph replays need no clearing); two split launches must not run at the same time on
-// one GPU (launches on the one library stream are ordered).
-constexpr int PART_FLOATS = 66;
-constexpr int SPLIT_MAX_UNITS = 4096;
-constexpr long SPLIT_SCRATCH_FLOATS = 8L << 20;  // 32 MB
-constexpr int SPLIT_SCAN = 512;                  // longest tile list the adaptive split scans
-constexpr int SPLIT_SPIN_LIMIT = 1 << 24;        // bounded wait for the partner's partial
-__device__ float g_split_part[SPLIT_SCRATCH_FLOATS];
-__device__ int g_split_sync[2 * SPLIT_MAX_UNITS];
 
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
@@ -110,8 +89,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
                         const int *__restrict__ ctx_lens, const int *__restrict__ cu_q,
                         const int *__restrict__ tile_seq, const int *__restrict__ tile_q0, int n_tiles, int nq,
                         int nkv, int G, int head_groups, int max_blocks, int block_size, int bs_shift,
-                        float scale_log2, float *__restrict__ part, int *__restrict__ sync, int split_min,
-                        int n_split, int slots) {
+                        float scale_log2) {
     constexpr int LOADS = 16 / NW;  // 4-row DMA instructions per wave per tile, for K and for V each
 
     __shared__ __attribute__((aligned(16))) bf16_t K0[TILE];
@@ -119,11 +97,9 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
     __shared__ __attribute__((aligned(16))) bf16_t K1[TILE];
     __shared__ __attribute__((aligned(16))) bf16_t V1[TILE];
 
-    // the first n_split workgroups are the second halves of units 0 .. n_split-1 (the heaviest)
-    const int half = (int)blockIdx.x < n_split ? 1 : 0;
-    const int unit = half ? (int)blockIdx.x : (int)blockIdx.x - n_split;
-    const int kvh = unit % nkv;
-    const int rest = unit / nkv;
+    const int bid = blockIdx.x;
+    const int kvh = bid % nkv;
+    const int rest = bid / nkv;
     const int hg = rest % head_groups;
     const int tile = n_tiles - 1 - rest / head_groups;
     const int s = tile_seq[tile], q0 = tile_q0[tile];
@@ -136,7 +112,6 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
 
     if (q_len == 1) return;  // single-row segments (decode rows of a mixed step): streamed by the decode kernel
     if (ctx < q_len) {       // padding sequence: zero rows, no keys (cpu/attention.zig:80-83)
-        if (half) return;
         const int row = r0 + l32;
         if (row < q_len) {
             bf16_t *o = out + ((long)(q_beg + row) * nq + head) * HD + hh * 64;
@@ -151,38 +126,6 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
     const int base_pos = ctx - q_len;                // position of segment row 0
     const int kend = base_pos + min(q0 + BQ, q_len);  // keys needed by the whole tile
     const int n_iter = (kend + BK - 1) / BK;
-    // key range of this workgroup: a split unit's halves take tiles [0, mid) and [mid, n_iter).  Every valid row
-    // sees at least one key in each half: its position is at least kend - BK, past mid * BK once n_iter >= 4.
-    // split_min > 0: split from that many key tiles on.  split_min == 0: split a unit only when it has more key
-    // tiles than a CU slot's share of the whole launch (then it would outlast the others); the candidates find
-    // the launch's total with one scan of the tile list (at most SPLIT_SCAN tiles, two memory round trips).
-    bool split = false;
-    if (unit < n_split) {
-        if (split_min > 0) {
-            split = n_iter >= split_min;
-        } else if (n_iter >= 4) {
-            int ts[SPLIT_SCAN / 64], tq[SPLIT_SCAN / 64];
-#pragma unroll
-            for (int c = 0; c < SPLIT_SCAN / 64; ++c) {
-                const int tt = c * 64 + lane;
-                ts[c] = tt < n_tiles ? tile_seq[tt] : -1;
-                tq[c] = tt < n_tiles ? tile_q0[tt] : 0;
-            }
-            int tot = 0;
-#pragma unroll
-            for (int c = 0; c < SPLIT_SCAN / 64; ++c) {
-                if (ts[c] < 0) continue;
-                const int b = cu_q[ts[c]], ql = cu_q[ts[c] + 1] - b, cx = ctx_lens[ts[c]];
-                if (ql > 1 && cx >= ql) tot += (cx - ql + min(tq[c] + BQ, ql) + BK - 1) / BK;
-            }
-#pragma unroll
-            for (int m = 32; m >= 1; m >>= 1) tot += __shfl_xor(tot, m);
-            split = (long)n_iter * slots > (long)tot * nkv * head_groups;
-        }
-    }
-    if (half && !split) return;
-    const int mid = n_iter / 2;
-    const int it_lo = (split && half) ? mid : 0, it_hi = (split && !half) ? mid : n_iter;
 
     // ---- Q fragments (B operand): lane holds row r0+l32, dims c*16 + hh*8 .. +8 ----
     const int my_row = r0 + l32;
@@ -392,65 +335,19 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
 
     // two LDS stages; the loop is unrolled twice so every DMA targets a fixed buffer (the compiler can then see
     // that the reads of one stage never wait for the DMA into the other)
-    if (it_lo < it_hi) issue(it_lo, K0, V0);
+    if (n_iter > 0) issue(0, K0, V0);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    for (int it = it_lo; it < it_hi; it += 2) {
-        if (it + 1 < it_hi) issue(it + 1, K1, V1);
+    for (int it = 0; it < n_iter; it += 2) {
+        if (it + 1 < n_iter) issue(it + 1, K1, V1);
         compute(it, K0, V0);
         __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA into stage 1 has landed
         __syncthreads();                // ... and everyone's; everyone is done reading stage 0
-        if (it + 1 >= it_hi) break;
-        if (it + 2 < it_hi) issue(it + 2, K0, V0);
+        if (it + 1 >= n_iter) break;
+        if (it + 2 < n_iter) issue(it + 2, K0, V0);
         compute(it + 1, K1, V1);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-    }
-
-    if (split) {
-        // ---- key-split merge.  The arrival counter elects the roles: the first workgroup stores its partial
-        //      with device-coherent stores, waits for them to complete and raises the ready flag; the second
-        //      waits for the flag (its partner is past its last barrier and waits for nothing, so the wait
-        //      ends), reads the partial with device-coherent loads, merges, and resets both sync words. ----
-        __shared__ int s_role;
-        int *cnt = sync + 2 * unit;
-        if (tid == 0) s_role = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __syncthreads();
-        float *pp = part + ((long)unit * NW + wave) * (64 * PART_FLOATS) + lane;
-        if (s_role == 0) {
-            if (wave_active) {
-#pragma unroll
-                for (int i = 0; i < 64; ++i)
-                    __hip_atomic_store(pp + i * 64, o[i >> 4][i & 15], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(pp + 64 * 64, m_run, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(pp + 65 * 64, l_run, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-            __builtin_amdgcn_s_waitcnt(0);
-            __syncthreads();
-            if (tid == 0) __hip_atomic_store(cnt + 1, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-            return;
-        }
-        if (tid == 0) {
-            for (int spin = 0; spin < SPLIT_SPIN_LIMIT; ++spin) {
-                if (__hip_atomic_load(cnt + 1, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
-                __builtin_amdgcn_s_sleep(2);
-            }
-            __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(cnt + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        __syncthreads();
-        if (!wave_active) return;
-        // lane-wise merge: both halves hold the same (row, dims) in the same lane; m is per row (base 2)
-        const float pm = __hip_atomic_load(pp + 64 * 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const float pl = __hip_atomic_load(pp + 65 * 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const float M = fmaxf(m_run, pm);
-        const float a = fast_exp2(m_run - M), b = fast_exp2(pm - M);
-#pragma unroll
-        for (int i = 0; i < 64; ++i) {
-            const float po = __hip_atomic_load(pp + i * 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            o[i >> 4][i & 15] = o[i >> 4][i & 15] * a + po * b;
-        }
-        l_run = l_run * a + pl * b;
     }
 
     // ---- normalise and store: lane holds dims db*32 + (r/4)*8 + hh*4 + r%4 of row my_row ----
@@ -470,63 +367,13 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
         }
 }
 
-// The key-split scratch of the current device (nullptrs if the addresses cannot be taken).
-struct SplitScratch {
-    float *part = nullptr;
-    int *sync = nullptr;
-};
-SplitScratch split_scratch() {
-    static SplitScratch cache[64];
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return {};
-    if (!cache[dev].part) {
-        void *p = nullptr, *q = nullptr;
-        if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_split_part)) != hipSuccess ||
-            hipGetSymbolAddress(&q, HIP_SYMBOL(g_split_sync)) != hipSuccess)
-            return {};
-        cache[dev] = {(float *)p, (int *)q};
-    }
-    return cache[dev];
-}
-
-// Split candidates: the units of the heaviest tiles, about half a CU-slot's worth, when the launch has fewer than
-// 2 units per slot and a tile list the kernel can scan (larger launches keep their slots full to the end; a 4096-
-// row chunk over a 12288-token history, 2 units per slot, measured 2-8 % slower with candidates).
-// LLMGEN_PREFILL_SPLIT (read at each launch): 0 = off; n >= 4 = every unit that fits the scratch is a candidate
-// and splits from n key tiles on (small cases for tests).
-long split_units(int NW, long units, int n_tiles, int nkv, int head_groups, long slots, int *split_min) {
-    const char *v = getenv("LLMGEN_PREFILL_SPLIT");
-    const int env = v && *v ? atoi(v) : -1;
-    *split_min = env >= 4 ? env : 0;
-    if (env == 0) return 0;
-    long n;
-    if (env >= 4) {
-        n = units;
-    } else {
-        if (units >= 2 * slots || n_tiles > SPLIT_SCAN) return 0;
-        n = std::min(units, std::max(1L, slots / 2 / (nkv * head_groups)) * nkv * head_groups);
-    }
-    n = std::min<long>(n, SPLIT_MAX_UNITS);
-    while (n > 0 && n * NW * 64 * PART_FLOATS > SPLIT_SCRATCH_FLOATS) n -= (long)nkv * head_groups;
-    return std::max(0L, n);
-}
-
 template <int NW, int MODE>
 void launch_prefill_mode(long grid, bf16_t *out, const bf16_t *q, const bf16_t *kc, const bf16_t *vc, const int *bt,
                          const int *ctx, const int *cu_q, const int *tile_seq, const int *tile_q0, int n_tiles, int nq,
                          int nkv, int G, int head_groups, int max_blocks, int block_size, int bs_shift, float sl2) {
-    const long slots = (long)llmgen_num_cus() * (NW == 8 ? 1 : 2);  // resident workgroups (LDS, registers)
-    int split_min = 0;
-    long n_split = split_units(NW, grid, n_tiles, nkv, head_groups, slots, &split_min);
-    SplitScratch sc{};
-    if (n_split > 0) {
-        sc = split_scratch();
-        if (!sc.part) n_split = 0;
-    }
-    hipLaunchKernelGGL((attn_prefill_kernel<NW, MODE>), dim3((unsigned)(grid + n_split)), dim3(64 * NW), 0,
-                       g_llmgen_stream, out, q, kc, vc, bt, ctx, cu_q, tile_seq, tile_q0, n_tiles, nq, nkv, G,
-                       head_groups, max_blocks, block_size, bs_shift, sl2, sc.part, sc.sync, split_min,
-                       (int)n_split, (int)slots);
+    hipLaunchKernelGGL((attn_prefill_kernel<NW, MODE>), dim3((unsigned)grid), dim3(64 * NW), 0, g_llmgen_stream, out, q,
+                       kc, vc, bt, ctx, cu_q, tile_seq, tile_q0, n_tiles, nq, nkv, G, head_groups, max_blocks,
+                       block_size, bs_shift, sl2);
 }
 
 template <int NW>

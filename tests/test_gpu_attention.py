@@ -278,14 +278,10 @@ def test_c5d_block_permutation_invariance(gpu):
     assert_cache_equal(to_u16(vc1), to_u16(vc0[inv]), "permuted V cache")
 
 
-def test_c5p_chunked_prefill_equals_tail(gpu, monkeypatch):
+def test_c5p_chunked_prefill_equals_tail(gpu):
     """Full c5p (16384-token prompt): prefilling the last 4096 tokens as a chunk against the cached first 12288
-    gives exactly the last 4096 rows of the full prefill (each row's keys, order and arithmetic are the same).
-    The key split is off for this check: it changes the summation order of the units it splits (its own tests
-    hold it to the oracle and to the unsplit kernel)."""
+    gives exactly the last 4096 rows of the full prefill (each row's keys, order and arithmetic are the same)."""
     import copy as _copy
-
-    monkeypatch.setenv("LLMGEN_PREFILL_SPLIT", "0")
 
     from llmgen_amd.step import Entry
 
@@ -412,25 +408,3 @@ def test_scores_growing_along_the_keys(gpu, name):
     _, _, _, of = run_oracle(wl, t)
     compare(to_u16(out), of, f"{name} growing scores")
 
-
-@pytest.mark.parametrize("name", ["gqa1", "gqa2", "gqa8", "gqa16", "bs48", "c3"])
-def test_prefill_key_split(gpu, name, monkeypatch):
-    """Key-split prefill (two workgroups per unit, cross-workgroup log-sum-exp merge through the library's scratch)
-    against the oracle and the unsplit kernel.  Small cases force the split of every unit with at least 4 key
-    tiles; c3 takes the launcher's own choice (its heaviest units).  Two launches in a row: the merge's sync words
-    must be back at zero after each."""
-    wl = make(name)
-    print(f"[gpu-test] {name}", flush=True)
-    t = wl.tensors(device="cuda")
-    monkeypatch.setenv("LLMGEN_PREFILL_SPLIT", "0")
-    ref = to_u16(run_gpu(wl, t)[0])
-    monkeypatch.setenv("LLMGEN_PREFILL_SPLIT", "-1" if name == "c3" else "4")
-    outs = [to_u16(run_gpu(wl, t)[0]) for _ in range(2)]
-    meta = wl.meta(lib().hip_attn_prefill_tile())
-    rows = _sample_rows(wl, meta) if name == "c3" else None
-    _, _, _, of = run_oracle(wl, t, rows=rows, threads=16)
-    r = oracle.bf16_to_f32(ref).astype(np.float64)
-    for got in outs:
-        compare(got if rows is None else got[rows], of, f"{name} split")
-        d = np.abs(oracle.bf16_to_f32(got).astype(np.float64) - r)
-        assert d.max() <= 8e-3, f"{name}: split vs unsplit max diff {d.max():.3g}"
