@@ -12,7 +12,8 @@
 //     rows' cache block.  Buffer (MUBUF) rather than FLAT-encoded global_load_lds: a FLAT load that writes LDS
 //     makes the compiler wait for every LDS read in flight (lgkmcnt(0)) wherever it waits for one, which
 //     serialises the fragment reads below.  Two LDS stages: tile t+1 streams in while tile t is computed, one
-//     barrier per tile.  Rows are stored as 16 chunks of 16 bytes with the chunk index XOR-swizzled by the row
+//     barrier per tile (one stage for the 2-wave workgroups of G = 1, so that four share a CU and hide each other's
+//     DMA).  Rows are stored as 16 chunks of 16 bytes with the chunk index XOR-swizzled by the row
 //     (K: row & 15, V: 4*row & 15) so the fragment reads below are bank-conflict free;
 //   * each wave owns 32 query rows of one head and computes S^T = K Q^T with v_mfma_f32_32x32x16_bf16: K
 //     (ds_read_b128 from LDS, issued KPF MFMA pairs ahead of use) is the A operand, Q (registers, loaded once)
@@ -83,7 +84,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const bf16_t *base, 
 
 // NW = waves per workgroup (2 per head: rows 0-31 and 32-63 of the tile); MODE = DmaMode.
 template <int NW, int MODE>
-__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW == 2 ? 1 : 2)))
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)))
     attn_prefill_kernel(bf16_t *__restrict__ out, const bf16_t *__restrict__ q, const bf16_t *__restrict__ kc,
                         const bf16_t *__restrict__ vc, const int *__restrict__ block_tables,
                         const int *__restrict__ ctx_lens, const int *__restrict__ cu_q,
@@ -94,8 +95,10 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
 
     __shared__ __attribute__((aligned(16))) bf16_t K0[TILE];
     __shared__ __attribute__((aligned(16))) bf16_t V0[TILE];
-    __shared__ __attribute__((aligned(16))) bf16_t K1[TILE];
-    __shared__ __attribute__((aligned(16))) bf16_t V1[TILE];
+    // 2-wave workgroups (G = 1) keep one stage: 32 KB of LDS lets four of them share a CU (two waves per SIMD)
+    constexpr bool ONE_STAGE = NW == 2;
+    __shared__ __attribute__((aligned(16))) bf16_t K1[ONE_STAGE ? 8 : TILE];
+    __shared__ __attribute__((aligned(16))) bf16_t V1[ONE_STAGE ? 8 : TILE];
 
     const int bid = blockIdx.x;
     const int kvh = bid % nkv;
@@ -335,19 +338,29 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
 
     // two LDS stages; the loop is unrolled twice so every DMA targets a fixed buffer (the compiler can then see
     // that the reads of one stage never wait for the DMA into the other)
-    if (n_iter > 0) issue(0, K0, V0);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    for (int it = 0; it < n_iter; it += 2) {
-        if (it + 1 < n_iter) issue(it + 1, K1, V1);
-        compute(it, K0, V0);
-        __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA into stage 1 has landed
-        __syncthreads();                // ... and everyone's; everyone is done reading stage 0
-        if (it + 1 >= n_iter) break;
-        if (it + 2 < n_iter) issue(it + 2, K0, V0);
-        compute(it + 1, K1, V1);
+    if (ONE_STAGE) {
+        for (int it = 0; it < n_iter; ++it) {
+            issue(it, K0, V0);
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();  // the tile has landed for every wave
+            compute(it, K0, V0);
+            __syncthreads();  // every wave is done reading it
+        }
+    } else {
+        if (n_iter > 0) issue(0, K0, V0);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
+        for (int it = 0; it < n_iter; it += 2) {
+            if (it + 1 < n_iter) issue(it + 1, K1, V1);
+            compute(it, K0, V0);
+            __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA into stage 1 has landed
+            __syncthreads();                // ... and everyone's; everyone is done reading stage 0
+            if (it + 1 >= n_iter) break;
+            if (it + 2 < n_iter) issue(it + 2, K0, V0);
+            compute(it + 1, K1, V1);
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+        }
     }
 
     // ---- normalise and store: lane holds dims db*32 + (r/4)*8 + hh*4 + r%4 of row my_row ----
