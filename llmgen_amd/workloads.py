@@ -14,7 +14,8 @@ Configurations (shape Qwen3-0.6B unless stated: 16 Q heads, 8 KV heads, head_dim
   c5p prefill, 32 Q / 8 KV heads, one 16384-token causal prompt, permuted blocks, std 1
 Reference test cases (src/backend/cuda/kernel_test.zig:151-232, src/backend/cpu/attention.zig:188-251) are
 ``kt_prefill``, ``kt_decode`` and ``cpu_mixed``, with U(-1, 1) inputs from a seeded generator.  Further small
-steps cover other GQA group sizes (``gqa*``) and block sizes 48 and 6 (``bs48*``, ``bs6*``).
+steps cover other GQA group sizes (``gqa*``), block sizes 48 and 6 (``bs48*``, ``bs6*``) and G = 1 at block sizes 6
+and 256 (``g1bs*``).
 """
 from __future__ import annotations
 
@@ -250,6 +251,19 @@ def make(name: str, seed: Optional[int] = None) -> Workload:
         return Workload(name, 8, 4, 128, 6, nb, 24, 144, ents, std=1.0, seed=s,
                         decode=None if name == "bs6d" else False,
                         note=f"block size 6, GQA 2 ({'decode' if name == 'bs6d' else 'mixed'})")
+    if name in ("g1bs6", "g1bs256"):
+        # G = 1 (the one-LDS-stage prefill kernel) with the per-lane DMA path (bs 6) and the one-descriptor-per-
+        # tile path (bs 256): prompts long enough for many key tiles, a chunked tail, decode rows
+        s = {"g1bs6": 51, "g1bs256": 52}[name] if seed is None else seed
+        bs = 6 if name == "g1bs6" else 256
+        rng = np.random.default_rng(s)
+        spec = [(0, 700), (300, 333), (521, 1), (0, 1)]
+        ctxs = [a + b for a, b in spec]
+        tables, nb = _tables(rng, ctxs, bs, permute=True, extra_blocks=2)
+        ents = [Entry(a, b, t) for (a, b), t in zip(spec, tables)]
+        mb = max(len(t) for t in tables)
+        return Workload(name, 4, 4, 128, bs, nb, mb, mb * bs, ents, std=1.0, seed=s, decode=False,
+                        note=f"GQA 1, block size {bs}, 700-token prompt + chunked tail + decode rows")
     raise KeyError(name)
 
 

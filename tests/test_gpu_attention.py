@@ -35,7 +35,8 @@ def _sample_rows(wl, meta, n_random=48, seed=0):
 
 
 @pytest.mark.parametrize("name", ["kt_prefill", "cpu_mixed", "c1", "c2", "gqa1", "gqa8", "gqa16",
-                                  "gqa1d", "gqa8d", "gqa16d", "bs48", "bs48d", "bs6", "bs6d", "gqa2"])
+                                  "gqa1d", "gqa8d", "gqa16d", "bs48", "bs48d", "bs6", "bs6d", "gqa2",
+                                  "g1bs6", "g1bs256"])
 def test_step_matches_oracle_all_rows(gpu, name):
     wl = make(name)
     print(f"[gpu-test] {name}", flush=True)
