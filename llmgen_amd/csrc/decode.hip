@@ -60,10 +60,12 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(G >
     constexpr int NTH = 64 * W;
     const int kvh = blockIdx.x, part = blockIdx.z;
     // decode launch: blockIdx.y is the sequence and its query row.  Prefill-metadata launch (cu_q != null):
-    // blockIdx.y is a query tile; only single-row segments (decode rows of a mixed step) are handled here.
+    // blockIdx.y counts query tiles from the end of the list; only single-row segments (decode rows of a mixed
+    // step) are handled here.  The tile list runs lightest first (by key end), so the longest contexts are
+    // dispatched first and the shortest fill the tail.
     int s = blockIdx.y, row = blockIdx.y;
     if (cu_q) {
-        s = tile_seq[blockIdx.y];
+        s = tile_seq[gridDim.y - 1 - blockIdx.y];
         row = cu_q[s];
         if (cu_q[s + 1] - row != 1) return;
     }
