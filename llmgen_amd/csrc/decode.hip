@@ -258,14 +258,23 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(G >
     };
 
     if (PIPE) {
+        // Loads are never conditional inside the loop body: a load issued under a branch makes the compiler
+        // wait for every outstanding load (vmcnt(0)) after the branch, which would serialise the two buffers.
         Buf bufA, bufB;
         load(0, bufA);
-        for (int r = 0; r < rounds; r += 2) {
-            if (r + 1 < rounds) load(r + 1, bufB);
+        int r = 0;
+        for (; r + 2 < rounds; r += 2) {  // rounds r + 1 and r + 2 exist
+            load(r + 1, bufB);
             compute(r, bufA);
-            if (r + 1 >= rounds) break;
-            if (r + 2 < rounds) load(r + 2, bufA);
+            load(r + 2, bufA);
             compute(r + 1, bufB);
+        }
+        if (r + 1 < rounds) {
+            load(r + 1, bufB);
+            compute(r, bufA);
+            compute(r + 1, bufB);
+        } else if (r < rounds) {
+            compute(r, bufA);
         }
     } else {  // one buffer, twice the occupancy: short spans rely on other waves to hide latency
         Buf buf;
@@ -482,11 +491,11 @@ int *merge_counters() {
     return ptr[dev];
 }
 
-// single-buffered rounds at 3-4 waves per SIMD measure faster than register double buffering at 2 (c2, c5d);
-// GQA groups of 8+ need the registers for o anyway
+// Register double buffering only for G = 16 (one 16-token tile per wave, so two buffers fit beside o; 7 % faster
+// at 32K context).  Single-buffered rounds measure faster at G <= 4 (c2, c5d), and at G = 8 the two buffers spill.
 bool use_pipe(int G) {
     static const int pipe_env = env_int("LLMGEN_DECODE_PIPE", -1);
-    return pipe_env >= 0 ? pipe_env != 0 : G >= 8;
+    return pipe_env >= 0 ? pipe_env != 0 : G >= 16;
 }
 
 // Waves per workgroup: 8 when the launch has enough (sequence, kv head) pairs to fill the chip with 8-wave
