@@ -31,6 +31,12 @@
 
 namespace {
 
+// V rows are read once, whole (four full 256-byte rows per instruction): a nontemporal load keeps them from
+// displacing cache lines.  K stays an ordinary load: its MFMA layout reads each 128-byte line in two halves by two
+// consecutive instructions, and the second half must still find the line in cache.
+__device__ __forceinline__ u32x4_t ld16_stream(const void *p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
+}
 constexpr int HD = 128;
 constexpr int DEC_THREADS = 256;  // the separate merge kernel's workgroup
 
@@ -177,7 +183,7 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(G >
             const int off = vt[j] - blk_index<POW2>(vt[j], block_size, bs_shift) * block_size;
             const bf16_t *vr = vbase + (long)vblk[j] * blk_stride + (long)off * HD + col * 8;
             if (fuse && vt[j] == ctx - 1) vr = v_new + new_row + col * 8;
-            b.vf[j] = ld16(vr);
+            b.vf[j] = ld16_stream(vr);
         }
     };
 
