@@ -8,8 +8,9 @@
 //
 // Design (one workgroup = one (kv head, sequence, span of parts), 4 or 8 waves):
 //   * every wave owns 16-token tiles of the part; per round a wave issues all of its K and V loads at once as
-//     16-byte vectors (K: the MFMA B-operand layout, 16 tokens x 64 B per instruction; V: 4 full 256-byte rows
-//     per instruction), so a workgroup keeps up to 128 KB in flight;
+//     16-byte nontemporal vectors, four whole 256-byte rows per instruction, so a workgroup keeps up to 128 KB in
+//     flight.  K rows then pass through a wave-private LDS slice into the MFMA B-operand layout (16 tokens x 64 B
+//     per fragment); loading that layout directly reads each 128-byte line in two halves, which streams worse;
 //   * QK^T runs on the matrix cores: v_mfma_f32_16x16x32_bf16 with the G query heads of the group as the 16 A
 //     rows, so the K bytes are read once for all G heads (GQA sharing).  Scores land one token per lane column,
 //     one head per row, and the softmax max / sum reduce over a 16-lane DPP row;
@@ -33,9 +34,8 @@
 
 namespace {
 
-// V rows are read once, whole (four full 256-byte rows per instruction): a nontemporal load keeps them from
-// displacing cache lines.  K stays an ordinary load: its MFMA layout reads each 128-byte line in two halves by two
-// consecutive instructions, and the second half must still find the line in cache.
+// K and V rows are read once, whole (four full 256-byte rows per instruction): nontemporal loads keep them from
+// displacing cache lines (c5d 362 -> 330 us).
 __device__ __forceinline__ u32x4_t ld16_stream(const void *p) {
     return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
 }
@@ -53,7 +53,7 @@ __device__ __forceinline__ int blk_index(int t, int block_size, int bs_shift) {
 // streams `span` tokens of one (kv head, sequence) pair.  PIPE: round r+1's block-table and K/V loads are issued
 // before round r is computed (register double buffering); otherwise one buffer and higher occupancy.
 template <int G, int NT, bool POW2, bool PIPE, bool FUSE, int W>
-__global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(G >= 16 ? 1 : (PIPE || G >= 8 ? 2 : (G >= 4 ? 3 : 4)))))
+__global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(G >= 16 ? 1 : (PIPE || G >= 8 ? 2 : 3))))
     attn_decode_split_kernel(bf16_t *__restrict__ out, float *__restrict__ part_o, float *__restrict__ part_ml,
                              const bf16_t *__restrict__ q, const bf16_t *__restrict__ kc,
                              const bf16_t *__restrict__ vc, const int *__restrict__ block_tables,
@@ -108,6 +108,7 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(G >
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 15, rgrp = lane >> 4;
 
+    __shared__ u32x4_t k_lds[W][WTOK][16];  // K rows of this round, 16-byte chunks XOR-swizzled by the token
     __shared__ float p_lds[W][WTOK][G];
     __shared__ float corr_lds[W][G];
     __shared__ float o_lds[W][G][HD];
@@ -143,16 +144,14 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(G >
 #pragma unroll
         for (int k = 0; k < 8; ++k) o[g][k] = 0.f;
 
-    // K: tile tau, chunk c = dims c*32 + rgrp*8 of token col; V: token rgrp + 4j, dims col*8.
+    // K and V: token rgrp + 4j, dims col*8 (four whole 256-byte rows per load instruction).
     struct Buf {
-        u32x4_t kf[NT][4];
+        u32x4_t kr[4 * NT];
         u32x4_t vf[4 * NT];
     };
     auto load = [&](int r, Buf &b) {
         const int wbase = r * RTOK + wave * WTOK;
-        int kt[NT], vt[4 * NT], kblk[NT], vblk[4 * NT];
-#pragma unroll
-        for (int tau = 0; tau < NT; ++tau) kt[tau] = t0 + min(wbase + tau * 16 + col, n - 1);
+        int vt[4 * NT], vblk[4 * NT];
 #pragma unroll
         for (int j = 0; j < 4 * NT; ++j) vt[j] = t0 + min(wbase + rgrp + 4 * j, n - 1);
         if (POW2 && block_size >= WTOK) {
@@ -162,23 +161,18 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(G >
             const int b1 = __builtin_amdgcn_readfirstlane((t0 + min(wbase + WTOK - 1, n - 1)) >> bs_shift);
             const int p0 = bt[b0], p1 = bt[b1];
 #pragma unroll
-            for (int tau = 0; tau < NT; ++tau) kblk[tau] = (kt[tau] >> bs_shift) == b0 ? p0 : p1;
-#pragma unroll
             for (int j = 0; j < 4 * NT; ++j) vblk[j] = (vt[j] >> bs_shift) == b0 ? p0 : p1;
         } else {
             // all block-table reads first (independent), then all K/V reads
 #pragma unroll
-            for (int tau = 0; tau < NT; ++tau) kblk[tau] = bt[blk_index<POW2>(kt[tau], block_size, bs_shift)];
-#pragma unroll
             for (int j = 0; j < 4 * NT; ++j) vblk[j] = bt[blk_index<POW2>(vt[j], block_size, bs_shift)];
         }
 #pragma unroll
-        for (int tau = 0; tau < NT; ++tau) {
-            const int off = kt[tau] - blk_index<POW2>(kt[tau], block_size, bs_shift) * block_size;
-            const bf16_t *kr = kbase + (long)kblk[tau] * blk_stride + (long)off * HD + rgrp * 8;
-            if (fuse && kt[tau] == ctx - 1) kr = k_new + new_row + rgrp * 8;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) b.kf[tau][c] = ld16(kr + c * 32);
+        for (int j = 0; j < 4 * NT; ++j) {
+            const int off = vt[j] - blk_index<POW2>(vt[j], block_size, bs_shift) * block_size;
+            const long row = (long)vblk[j] * blk_stride + (long)off * HD + col * 8;
+            const bool mine = fuse && vt[j] == ctx - 1;
+            b.kr[j] = ld16_stream(mine ? k_new + new_row + col * 8 : kbase + row);
         }
 #pragma unroll
         for (int j = 0; j < 4 * NT; ++j) {
@@ -191,6 +185,24 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(G >
 
     auto compute = [&](int r, const Buf &b) {
         const int wbase = r * RTOK + wave * WTOK;
+        // ---- K rows into this wave's LDS slice, then the MFMA B fragments back out of it (tile tau, chunk c =
+        //      dims c*32 + rgrp*8 of token tau*16 + col); the XOR swizzle keeps both directions conflict-free ----
+#pragma unroll
+        for (int j = 0; j < 4 * NT; ++j) {
+            const int tok = rgrp + 4 * j;
+            k_lds[wave][tok][col ^ (tok & 15)] = b.kr[j];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        u32x4_t kf[NT][4];
+#pragma unroll
+        for (int tau = 0; tau < NT; ++tau)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int tok = tau * 16 + col;
+                kf[tau][c] = k_lds[wave][tok][(c * 4 + rgrp) ^ (tok & 15)];
+            }
         // ---- scores on the matrix cores: D[g][token] = sum_d q[g][d] k[token][d] ----
         f32x4_t sc[NT];
 #pragma unroll
@@ -198,7 +210,7 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(G >
             f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int c = 0; c < 4; ++c)
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[c], __builtin_bit_cast(bf16x8_t, b.kf[tau][c]),
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[c], __builtin_bit_cast(bf16x8_t, kf[tau][c]),
                                                               acc, 0, 0, 0);
             const bool valid = wbase + tau * 16 + col < n;
 #pragma unroll
