@@ -623,7 +623,11 @@ void llmgen_decode_rows_of_prefill(bf16_t *out, const bf16_t *q, const bf16_t *k
     DecodeArgs a{out, q, k_cache, v_cache, block_tables, ctx_lens, nq, nkv, max_blocks, block_size,
                  (block_size & (block_size - 1)) == 0 ? __builtin_ctz(block_size) : -1, scale * LLMGEN_LOG2E,
                  nullptr, nullptr, 1 << 30, 1, 1, nullptr, cu_q, tile_seq, stream};
-    a.waves = decode_waves(G, (long)n_tiles * nkv);
+    // one workgroup per (row, kv head) and no split: many generations of workgroups per CU, which overlap their
+    // start and end better as 4-wave workgroups (c4 262 -> 249 us; the split decode launch sizes its grid to about
+    // one generation and prefers 8)
+    static const int forced = env_int("LLMGEN_DECODE_WAVES", 0);
+    a.waves = forced == 8 ? 8 : 4;
     launch_decode_rows(dim3(nkv, n_tiles, 1), a, G);
 }
 
