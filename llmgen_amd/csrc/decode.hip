@@ -17,7 +17,7 @@
 //   * softmax is in base 2 (scale * log2 e folded in), fp32 throughout; the probabilities go through a small
 //     per-wave LDS buffer to the PV lanes, which hold 8 head dims of 4 tokens per 16-byte V vector and
 //     accumulate all G heads in fp32 registers;
-//   * the four waves merge (max, sum, unnormalised o) through LDS; a part that is the only part of its
+//   * the W waves merge (max, sum, unnormalised o) through LDS; a part that is the only part of its
 //     sequence writes the final bf16 row directly, otherwise (o, m, l) go to the caller's scratch and the last
 //     workgroup of the (sequence, kv head) to finish merges the parts with the log-sum-exp rule
 //     (attention.cu:186-207), elected by a self-resetting counter (attn_decode_reduce_kernel when the launch
