@@ -409,3 +409,16 @@ def test_scores_growing_along_the_keys(gpu, name):
     _, _, _, of = run_oracle(wl, t)
     compare(to_u16(out), of, f"{name} growing scores")
 
+
+
+@pytest.mark.parametrize("name", ["c2", "gqa8d", "c1", "cpu_mixed", "c3"])
+def test_step_output_is_bit_reproducible(gpu, name):
+    """The same step run twice gives the same bits: each wave's token set and every merge order are fixed (no
+    dynamic work distribution, no atomics on values), for split-K decode with its cross-workgroup merge (c1,
+    gqa8d), batched decode (c2), a mixed step (cpu_mixed) and prefill (c3)."""
+    wl = make(name)
+    print(f"[gpu-test] {name}", flush=True)
+    t = wl.tensors(device="cuda")
+    outs = [to_u16(run_gpu(wl, t)[0]) for _ in range(3)]
+    np.testing.assert_array_equal(outs[1], outs[0])
+    np.testing.assert_array_equal(outs[2], outs[0])
