@@ -40,6 +40,13 @@ __device__ __forceinline__ u32x4_t ld16_stream(const void *p) {
     return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
 }
 constexpr int HD = 128;
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
+// LDS read with transpose: a 16-lane group whose lane 4j+m addresses four 16-bit values (dims 4m..4m+3) of row j
+// receives, in lane i, rows 0..3's value of dim i
+__device__ __forceinline__ s16x4_t ds_read_tr(const bf16_t *p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t *)p);
+}
 constexpr int DEC_THREADS = 256;  // the separate merge kernel's workgroup
 
 // Block-table lookup of logical token t (POW2: block_size == 1 << bs_shift).
@@ -53,7 +60,7 @@ __device__ __forceinline__ int blk_index(int t, int block_size, int bs_shift) {
 // streams `span` tokens of one (kv head, sequence) pair.  PIPE: round r+1's block-table and K/V loads are issued
 // before round r is computed (register double buffering); otherwise one buffer and higher occupancy.
 template <int G, int NT, bool POW2, bool PIPE, bool FUSE, int W>
-__global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(G >= 16 ? 1 : (PIPE || G >= 8 ? 2 : 3))))
+__global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(PIPE ? 2 : 3)))
     attn_decode_split_kernel(bf16_t *__restrict__ out, float *__restrict__ part_o, float *__restrict__ part_ml,
                              const bf16_t *__restrict__ q, const bf16_t *__restrict__ kc,
                              const bf16_t *__restrict__ vc, const int *__restrict__ block_tables,
@@ -109,7 +116,7 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(G >
     const int col = lane & 15, rgrp = lane >> 4;
 
     __shared__ u32x4_t k_lds[W][WTOK][16];  // K rows of this round, 16-byte chunks XOR-swizzled by the token
-    __shared__ float p_lds[W][WTOK][G];
+    __shared__ __attribute__((aligned(16))) float p_lds[W][WTOK][G];
     __shared__ float corr_lds[W][G];
     __shared__ float o_lds[W][G][HD];
     __shared__ float m_lds[W][G];
@@ -138,11 +145,17 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(G >
         m_run[i] = -INFINITY;
         l_run[i] = 0.f;
     }
+    // MPV (G >= 8, and every 8-wave workgroup): P V on the matrix cores; o4[db] is the 16 x 16 block (rows: heads rgrp*4 + i, columns: dims
+    // db*16 + col) of O.  Otherwise o[g][k]: dims col*8 + k of head g over this lane's tokens.
+    constexpr bool MPV = G >= 8 || W == 8;
     float o[G][8];
+    f32x4_t o4[8];
 #pragma unroll
     for (int g = 0; g < G; ++g)
 #pragma unroll
         for (int k = 0; k < 8; ++k) o[g][k] = 0.f;
+#pragma unroll
+    for (int db = 0; db < 8; ++db) o4[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
     // K and V: token rgrp + 4j, dims col*8 (four whole 256-byte rows per load instruction).
     struct Buf {
@@ -238,6 +251,55 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(G >
             l_run[i] = l_run[i] * corr[i] + sum;
             m_run[i] = m_new;
         }
+        if constexpr (MPV) {
+            // ---- P V on the matrix cores (v_mfma_f32_16x16x16_bf16): A = P (rows: heads, k: tokens) from this
+            //      wave's LDS slice laid out [head][token]; B = V (k: tokens, columns: dims) read transposed from the
+            //      wave's K slice, which now holds this round's V rows (the K fragments are in registers) ----
+            float *pw = &p_lds[wave][0][0];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int g = rgrp * 4 + i;
+                if (g < G) {
+#pragma unroll
+                    for (int tau = 0; tau < NT; ++tau) pw[g * WTOK + tau * 16 + col] = sc[tau][i];
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 4 * NT; ++j) {
+                const int t = rgrp + 4 * j;
+                k_lds[wave][t][col ^ ((t << 2) & 15)] = b.vf[j];
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+            for (int db = 0; db < 8; ++db)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) o4[db][i] *= corr[i];
+            const bf16_t *vb = reinterpret_cast<const bf16_t *>(&k_lds[wave][0][0]);
+            const int jj = col >> 2, mm = col & 3;
+#pragma unroll
+            for (int kb = 0; kb < NT; ++kb) {
+                f32x4_t pv = {0.f, 0.f, 0.f, 0.f};
+                if (col < G) pv = *reinterpret_cast<const f32x4_t *>(&pw[col * WTOK + kb * 16 + rgrp * 4]);
+                u32x2_t pa;
+                pa[0] = pack_bf16x2(pv[0], pv[1]);
+                pa[1] = pack_bf16x2(pv[2], pv[3]);
+                const s16x4_t a = __builtin_bit_cast(s16x4_t, pa);
+                const int key = kb * 16 + rgrp * 4 + jj;
+#pragma unroll
+                for (int db = 0; db < 8; ++db) {
+                    const int dim = db * 16 + 4 * mm;
+                    const int off = key * HD + (((dim >> 3) ^ ((key << 2) & 15)) << 3) + (dim & 7);
+                    o4[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, ds_read_tr(vb + off), o4[db], 0, 0, 0);
+                }
+            }
+            // the next round rewrites both slices: keep every lane's reads ahead of those writes
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            return;
+        }
         // probabilities to this wave's LDS slice (wave-private: a wavefront fence orders write -> read)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -317,20 +379,31 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(G >
             }
         }
     }
+    if constexpr (MPV) {
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+        for (int i = 0; i < 4; ++i) {
+            const int g = rgrp * 4 + i;
+            if (g < G) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            float x = o[g][k];
-            x += lane_xor(x, 16);
-            x += lane_xor(x, 32);
-            o[g][k] = x;
+                for (int db = 0; db < 8; ++db) o_lds[wave][g][db * 16 + col] = o4[db][i];
+            }
         }
-    if (lane < 16) {
+    } else {
 #pragma unroll
         for (int g = 0; g < G; ++g)
 #pragma unroll
-            for (int k = 0; k < 8; ++k) o_lds[wave][g][lane * 8 + k] = o[g][k];
+            for (int k = 0; k < 8; ++k) {
+                float x = o[g][k];
+                x += lane_xor(x, 16);
+                x += lane_xor(x, 32);
+                o[g][k] = x;
+            }
+        if (lane < 16) {
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int k = 0; k < 8; ++k) o_lds[wave][g][lane * 8 + k] = o[g][k];
+        }
     }
     __syncthreads();
 
@@ -511,11 +584,12 @@ int *merge_counters() {
     return ptr[dev];
 }
 
-// Register double buffering only for G = 16 (one 16-token tile per wave, so two buffers fit beside o; 7 % faster
-// at 32K context).  Single-buffered rounds measure faster at G <= 4 (c2, c5d), and at G = 8 the two buffers spill.
+// Register double buffering only on request (LLMGEN_DECODE_PIPE=1): single-buffered rounds at up to 3 waves per
+// SIMD measure as fast or faster for every group size (c2, c5d; G = 8 and 16 at 1K and 32K contexts).
 bool use_pipe(int G) {
     static const int pipe_env = env_int("LLMGEN_DECODE_PIPE", -1);
-    return pipe_env >= 0 ? pipe_env != 0 : G >= 16;
+    (void)G;
+    return pipe_env > 0;
 }
 
 // Waves per workgroup: 8 when the launch has enough (sequence, kv head) pairs to fill the chip with 8-wave
