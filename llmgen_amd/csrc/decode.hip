@@ -14,9 +14,10 @@
 //   * QK^T runs on the matrix cores: v_mfma_f32_16x16x32_bf16 with the G query heads of the group as the 16 A
 //     rows, so the K bytes are read once for all G heads (GQA sharing).  Scores land one token per lane column,
 //     one head per row, and the softmax max / sum reduce over a 16-lane DPP row;
-//   * softmax is in base 2 (scale * log2 e folded in), fp32 throughout; the probabilities go through a small
-//     per-wave LDS buffer to the PV lanes, which hold 8 head dims of 4 tokens per 16-byte V vector and
-//     accumulate all G heads in fp32 registers;
+//   * softmax is in base 2 (scale * log2 e folded in), fp32 throughout.  P V runs on the matrix cores for
+//     G >= 8 and in 8-wave workgroups (v_mfma_f32_16x16x16_bf16: P from a per-wave LDS slice as A, V^T read
+//     transposed out of the wave's LDS slice as B); otherwise the probabilities go through the per-wave LDS
+//     slice to PV lanes that hold 8 head dims of 4 tokens per 16-byte V vector and accumulate all G heads in fp32;
 //   * the W waves merge (max, sum, unnormalised o) through LDS; a part that is the only part of its
 //     sequence writes the final bf16 row directly, otherwise (o, m, l) go to the caller's scratch and the last
 //     workgroup of the (sequence, kv head) to finish merges the parts with the log-sum-exp rule
