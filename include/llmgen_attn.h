@@ -85,6 +85,24 @@ void hip_attn_prefill_rows(uint16_t *out, const uint16_t *q, const uint16_t *k_c
 /* Replaces cuda_attn_prefill_tile (attention_v1.zig:48): query rows per prefill tile (64). */
 int hip_attn_prefill_tile(void);
 
+/* Launcher options.  No reference counterpart except LLMGEN_OPT_ATTN_PART_MIN, which restates the reference's
+ * SV_ATTN_PART switch (attention.cu:219-229): split-K parts of at least that many tokens (0 = off; it can only
+ * lengthen parts, so max_parts and the scratch stay valid).  The others select paths that the default launch
+ * heuristics reach only on rare shapes, so that they can be tested and tuned:
+ *   LLMGEN_OPT_DECODE_ROW_WAVES    4 (default) or 8 waves per workgroup for the decode rows of a prefill step;
+ *   LLMGEN_OPT_DECODE_MERGE_KERNEL 1: merge split-K partials in a separate merge kernel (the path of launches with
+ *                                  more than 2^18 (sequence, kv head) pairs), 0 (default): in the decode kernel.
+ * Defaults are read from the environment (SV_ATTN_PART, LLMGEN_DECODE_ROW_WAVES, LLMGEN_DECODE_MERGE) on first
+ * use.  Returns the previous value, or -1 (and prints one line) for an unknown option or a bad value.  Not
+ * thread-safe; set options between launches. */
+enum {
+    LLMGEN_OPT_ATTN_PART_MIN = 0,
+    LLMGEN_OPT_DECODE_ROW_WAVES = 1,
+    LLMGEN_OPT_DECODE_MERGE_KERNEL = 2,
+    LLMGEN_OPT_COUNT = 3
+};
+int hip_attn_set_option(int option, int value);
+
 /* ---------------------------------------------------------------------------------------------------------
  * Device context (cuda_context.zig:1-11, cuda_context.cu:13-126)
  * ------------------------------------------------------------------------------------------------------- */

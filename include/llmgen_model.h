@@ -54,8 +54,8 @@ void hip_mul(uint16_t *out, const uint16_t *a, const uint16_t *b, size_t n);
 void hip_gather_rows(uint16_t *out, const uint16_t *x, const int32_t *idx, int S, int H);
 
 /* out_ids [S] = argmax over logits [S, V] bf16 per row: greedy when temps[s] <= 0 (the first index of the maximum),
- * else Gumbel-max of logits / temp with splitmix64 noise keyed by (*seed, s, index).  scratch: at least
- * hip_sample_scratch_bytes(S) bytes of device memory. */
+ * else Gumbel-max of logits / temp with splitmix64 noise keyed by (*seed, s, index).  No scratch is used:
+ * hip_sample_scratch_bytes returns 0 and scratch may be NULL (both kept for the reference's argument list). */
 void hip_sample(int32_t *out_ids, const uint16_t *logits, const float *temps, const uint64_t *seed, int S, int V,
                 void *scratch);
 size_t hip_sample_scratch_bytes(int max_S);

@@ -58,10 +58,10 @@ __device__ __forceinline__ int blk_index(int t, int block_size, int bs_shift) {
 
 // G = query heads per KV head (1..16); NT = 16-token tiles per wave per round (a round is W waves x 16*NT
 // tokens); W = waves per workgroup (4 or 8); FUSE = also write the step's token into the cache.  Each workgroup
-// streams `span` tokens of one (kv head, sequence) pair.  PIPE: round r+1's block-table and K/V loads are issued
-// before round r is computed (register double buffering); otherwise one buffer and higher occupancy.
-template <int G, int NT, bool POW2, bool PIPE, bool FUSE, int W>
-__global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(PIPE ? 2 : 3)))
+// streams `span` tokens of one (kv head, sequence) pair, one round at a time with a single register buffer
+// (three waves per SIMD hide each other's load latency).
+template <int G, int NT, bool POW2, bool FUSE, int W>
+__global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(3)))
     attn_decode_split_kernel(bf16_t *__restrict__ out, float *__restrict__ part_o, float *__restrict__ part_ml,
                              const bf16_t *__restrict__ q, const bf16_t *__restrict__ kc,
                              const bf16_t *__restrict__ vc, const int *__restrict__ block_tables,
@@ -340,31 +340,10 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(PIP
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     };
 
-    if (PIPE) {
-        // Loads are never conditional inside the loop body: a load issued under a branch makes the compiler
-        // wait for every outstanding load (vmcnt(0)) after the branch, which would serialise the two buffers.
-        Buf bufA, bufB;
-        load(0, bufA);
-        int r = 0;
-        for (; r + 2 < rounds; r += 2) {  // rounds r + 1 and r + 2 exist
-            load(r + 1, bufB);
-            compute(r, bufA);
-            load(r + 2, bufA);
-            compute(r + 1, bufB);
-        }
-        if (r + 1 < rounds) {
-            load(r + 1, bufB);
-            compute(r, bufA);
-            compute(r + 1, bufB);
-        } else if (r < rounds) {
-            compute(r, bufA);
-        }
-    } else {  // one buffer, twice the occupancy: short spans rely on other waves to hide latency
-        Buf buf;
-        for (int r = 0; r < rounds; ++r) {
-            load(r, buf);
-            compute(r, buf);
-        }
+    Buf buf;
+    for (int r = 0; r < rounds; ++r) {
+        load(r, buf);
+        compute(r, buf);
     }
 
     // ---- per-wave totals ----
@@ -528,10 +507,10 @@ struct DecodeArgs {
     int waves = 4;  // waves per workgroup (4 or 8)
 };
 
-template <int G, int NT, bool POW2, bool PIPE, int W>
+template <int G, int NT, bool POW2, int W>
 void launch_split_w(dim3 grid, const DecodeArgs &a) {
-    auto kern = a.k_new ? attn_decode_split_kernel<G, NT, POW2, PIPE, true, W>
-                        : attn_decode_split_kernel<G, NT, POW2, PIPE, false, W>;
+    auto kern = a.k_new ? attn_decode_split_kernel<G, NT, POW2, true, W>
+                        : attn_decode_split_kernel<G, NT, POW2, false, W>;
     hipLaunchKernelGGL(kern, grid, dim3(64 * W), 0,
                        a.stream ? a.stream : g_llmgen_stream, a.out,
                        a.part_o, a.part_ml, a.q, a.kc, a.vc, a.bt, a.ctx, a.nq, a.nkv, a.max_blocks, a.block_size,
@@ -539,33 +518,25 @@ void launch_split_w(dim3 grid, const DecodeArgs &a) {
                        a.v_new, a.slots, a.kc_w, a.vc_w);
 }
 
-template <int G, int NT, bool POW2, bool PIPE>
+template <int G, int NT, bool POW2>
 void launch_split(dim3 grid, const DecodeArgs &a) {
-    if (G <= 4 && a.waves == 8)
-        launch_split_w<G, NT, POW2, PIPE, 8>(grid, a);
-    else
-        launch_split_w<G, NT, POW2, PIPE, 4>(grid, a);
+    if constexpr (G <= 4) {
+        if (a.waves == 8) {
+            launch_split_w<G, NT, POW2, 8>(grid, a);
+            return;
+        }
+    }
+    launch_split_w<G, NT, POW2, 4>(grid, a);
 }
 
 template <int G, int NT>
-void launch_pow2(dim3 grid, const DecodeArgs &a, bool pipe) {
-    if (a.bs_shift >= 0) {
-        if (pipe)
-            launch_split<G, NT, true, true>(grid, a);
-        else
-            launch_split<G, NT, true, false>(grid, a);
-    } else {
-        if (pipe)
-            launch_split<G, NT, false, true>(grid, a);
-        else
-            launch_split<G, NT, false, false>(grid, a);
-    }
+void launch_pow2(dim3 grid, const DecodeArgs &a) {
+    if (a.bs_shift >= 0)
+        launch_split<G, NT, true>(grid, a);
+    else
+        launch_split<G, NT, false>(grid, a);
 }
 
-int env_int(const char *name, int dflt) {
-    const char *v = getenv(name);
-    return v && *v ? atoi(v) : dflt;
-}
 
 // Merge counters for the in-kernel split-K merge, one per (sequence, kv head).  They start at zero when the
 // library loads and every merging workgroup resets its own, so they are zero between launches.  Launches that
@@ -585,31 +556,20 @@ int *merge_counters() {
     return ptr[dev];
 }
 
-// Register double buffering only on request (LLMGEN_DECODE_PIPE=1): single-buffered rounds at up to 3 waves per
-// SIMD measure as fast or faster for every group size (c2, c5d; G = 8 and 16 at 1K and 32K contexts).
-bool use_pipe(int G) {
-    static const int pipe_env = env_int("LLMGEN_DECODE_PIPE", -1);
-    (void)G;
-    return pipe_env > 0;
-}
-
 // Waves per workgroup: 8 when the launch has enough (sequence, kv head) pairs to fill the chip with 8-wave
 // workgroups (fewer, longer workgroups: less split-K merging, fewer partial results), else 4.
 int decode_waves(int G, long pairs) {
-    static const int forced = env_int("LLMGEN_DECODE_WAVES", 0);
     if (G > 4) return 4;
-    if (forced == 4 || forced == 8) return forced;
     return pairs * 2 >= llmgen_num_cus() ? 8 : 4;
 }
 
 void launch_decode_rows(dim3 grid, const DecodeArgs &a, int G) {
-    const bool pipe = use_pipe(G);
     switch (G) {
-        case 1: launch_pow2<1, 2>(grid, a, pipe); break;
-        case 2: launch_pow2<2, 2>(grid, a, pipe); break;
-        case 4: launch_pow2<4, 2>(grid, a, pipe); break;
-        case 8: launch_pow2<8, 2>(grid, a, pipe); break;
-        default: launch_pow2<16, 1>(grid, a, pipe); break;
+        case 1: launch_pow2<1, 2>(grid, a); break;
+        case 2: launch_pow2<2, 2>(grid, a); break;
+        case 4: launch_pow2<4, 2>(grid, a); break;
+        case 8: launch_pow2<8, 2>(grid, a); break;
+        default: launch_pow2<16, 1>(grid, a); break;
     }
 }
 
@@ -633,12 +593,15 @@ void decode_launch(bf16_t *out, const bf16_t *q, const bf16_t *k_new, const bf16
         fprintf(stderr, "[llmgen-hip] attn_decode: unsupported GQA group size %d\n", G);
         return;
     }
+    // SV_ATTN_PART (attention.cu:219-229): parts only ever get longer, so max_parts slots still suffice
+    const int part_min = llmgen_opt(LLMGEN_OPT_ATTN_PART_MIN);
+    if (part_min > part_size) part_size = part_min;
     // Each workgroup takes k consecutive parts (span = k * part_size tokens, one partial result).  k grows
     // with the launch so that a long-context launch has about 8 waves per compute unit (two 4-wave or one
     // 8-wave workgroup), each streaming a long span, instead of many short workgroups; partial slots stay
     // < max_parts.
     const long total = (long)nkv * S * max_parts;
-    static const int wg_per_cu = env_int("LLMGEN_DECODE_WG_PER_CU", 2);
+    constexpr int wg_per_cu = 2;
     const int W = decode_waves(G, (long)S * nkv);
     const long target = (long)wg_per_cu * llmgen_num_cus() * 4 / W;
     // ... and a span is at least one round (W waves x 32 tokens, 16 at G = 16), so that no wave of a workgroup
@@ -646,10 +609,13 @@ void decode_launch(bf16_t *out, const bf16_t *q, const bf16_t *k_new, const bf16
     const int round_tokens = W * (G >= 16 ? 16 : 32);
     const int k = std::max((int)(total > target ? total / target : 1), (round_tokens + part_size - 1) / part_size);
     const int nparts = (max_parts + k - 1) / k;
-    int *counters = (long)S * nkv <= MAX_MERGE_SEGMENTS ? merge_counters() : nullptr;
+    int stride = max_parts;  // partial slots per (sequence, head) in part_o / part_ml
+    int *counters = (long)S * nkv <= MAX_MERGE_SEGMENTS && !llmgen_opt(LLMGEN_OPT_DECODE_MERGE_KERNEL)
+                        ? merge_counters()
+                        : nullptr;
     DecodeArgs a{out, q, k_cache, v_cache, block_tables, ctx_lens, nq, nkv, max_blocks, block_size,
                  (block_size & (block_size - 1)) == 0 ? __builtin_ctz(block_size) : -1, scale * LLMGEN_LOG2E,
-                 part_o, part_ml, part_size * k, max_parts, nparts, counters};
+                 part_o, part_ml, part_size * k, stride, nparts, counters};
     a.k_new = k_new;
     a.v_new = v_new;
     a.slots = slots;
@@ -659,7 +625,7 @@ void decode_launch(bf16_t *out, const bf16_t *q, const bf16_t *k_new, const bf16
     launch_decode_rows(dim3(nkv, S, nparts), a, G);
     if (!counters)  // batches beyond the counter array merge in a second kernel
         hipLaunchKernelGGL(attn_decode_reduce_kernel, dim3(nkv, S), dim3(DEC_THREADS), 0, g_llmgen_stream, out,
-                           part_o, part_ml, ctx_lens, nq, G, a.span, nparts, max_parts);
+                           part_o, part_ml, ctx_lens, nq, G, a.span, nparts, stride);
 }
 
 }  // namespace
@@ -701,8 +667,7 @@ void llmgen_decode_rows_of_prefill(bf16_t *out, const bf16_t *q, const bf16_t *k
     // one workgroup per (row, kv head) and no split: many generations of workgroups per CU, which overlap their
     // start and end better as 4-wave workgroups (c4 262 -> 249 us; the split decode launch sizes its grid to about
     // one generation and prefers 8)
-    static const int forced = env_int("LLMGEN_DECODE_WAVES", 0);
-    a.waves = forced == 8 ? 8 : 4;
+    a.waves = llmgen_opt(LLMGEN_OPT_DECODE_ROW_WAVES) == 8 ? 8 : 4;
     launch_decode_rows(dim3(nkv, n_tiles, 1), a, G);
 }
 

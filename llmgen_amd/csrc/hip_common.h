@@ -9,6 +9,8 @@
 #include <stdint.h>
 #include <stdio.h>
 
+#include "llmgen_attn.h"
+
 typedef uint16_t bf16_t;  // bf16 bit pattern as stored in memory
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
@@ -90,6 +92,9 @@ __attribute__((visibility("hidden"))) void llmgen_decode_rows_of_prefill(
 // kernels of one launcher concurrently; legal inside stream capture.
 __attribute__((visibility("hidden"))) hipStream_t llmgen_fork_side_stream();
 __attribute__((visibility("hidden"))) void llmgen_join_side_stream(hipStream_t side);
+
+// Internal: the value of a launcher option (LLMGEN_OPT_* of llmgen_attn.h), set by hip_attn_set_option.
+__attribute__((visibility("hidden"))) int llmgen_opt(int which);
 
 // Internal: compute units of the current device (256 if the query fails); cached after the first call.
 __attribute__((visibility("hidden"))) int llmgen_num_cus();

@@ -46,6 +46,33 @@ void llmgen_join_side_stream(hipStream_t side) {
     HIP_WARN(hipStreamWaitEvent(g_llmgen_stream, g_join_event, 0));
 }
 
+// Run-time options of the launchers (hip_attn_set_option).  Defaults come from the environment on first use:
+// SV_ATTN_PART (the reference's switch, attention.cu:219-229: the split-K part length is raised to at least this
+// many tokens), LLMGEN_DECODE_ROW_WAVES (4 or 8 waves per workgroup for the decode rows of a prefill step) and
+// LLMGEN_DECODE_MERGE (1: merge split-K partials in the separate merge kernel instead of in the decode kernel).
+static int g_opts[LLMGEN_OPT_COUNT];
+static bool g_opts_loaded = false;
+
+static void load_opts() {
+    if (g_opts_loaded) return;
+    auto env = [](const char *name, int dflt) {
+        const char *v = getenv(name);
+        return v && *v ? atoi(v) : dflt;
+    };
+    g_opts[LLMGEN_OPT_ATTN_PART_MIN] = env("SV_ATTN_PART", 0);
+    if (g_opts[LLMGEN_OPT_ATTN_PART_MIN] > 0)
+        fprintf(stderr, "[llmgen-hip] SV_ATTN_PART=%d: split-K parts of at least that many tokens\n",
+                g_opts[LLMGEN_OPT_ATTN_PART_MIN]);
+    g_opts[LLMGEN_OPT_DECODE_ROW_WAVES] = env("LLMGEN_DECODE_ROW_WAVES", 4);
+    g_opts[LLMGEN_OPT_DECODE_MERGE_KERNEL] = env("LLMGEN_DECODE_MERGE", 0);
+    g_opts_loaded = true;
+}
+
+int llmgen_opt(int which) {
+    load_opts();
+    return which >= 0 && which < LLMGEN_OPT_COUNT ? g_opts[which] : 0;
+}
+
 int llmgen_num_cus() {
     static int n = 0;
     if (n == 0) {
@@ -58,6 +85,25 @@ int llmgen_num_cus() {
 }
 
 extern "C" {
+
+int hip_attn_set_option(int option, int value) {
+    load_opts();
+    if (option < 0 || option >= LLMGEN_OPT_COUNT) {
+        fprintf(stderr, "[llmgen-hip] hip_attn_set_option: unknown option %d\n", option);
+        return -1;
+    }
+    if (option == LLMGEN_OPT_DECODE_ROW_WAVES && value != 4 && value != 8) {
+        fprintf(stderr, "[llmgen-hip] hip_attn_set_option: decode-row waves must be 4 or 8 (got %d)\n", value);
+        return -1;
+    }
+    if (value < 0) {
+        fprintf(stderr, "[llmgen-hip] hip_attn_set_option: negative value %d\n", value);
+        return -1;
+    }
+    const int prev = g_opts[option];
+    g_opts[option] = value;
+    return prev;
+}
 
 // cuda_context.cu:13-42.  Creates the global stream on device 0.  ws_bytes is accepted for signature parity
 // (the reference sizes a cuBLAS workspace with it); the attention path needs no library workspace.

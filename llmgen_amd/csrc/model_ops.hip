@@ -165,78 +165,84 @@ __global__ void gather_rows_kernel(bf16_t *out, const bf16_t *x, const int *idx,
 }
 
 // ---------------------------------------------------------------------------------------------- sampling
-// Phase 1: grid (S, SAMPLE_SPLIT); each workgroup finds (max, first index) over one contiguous chunk of the row.
-// Phase 2: one wave per row merges the SAMPLE_SPLIT candidates.  Merging keeps the larger value and, on equal
-// values, the smaller index, which is the reference's sequential "strictly greater" scan.  NaN never wins
-// (every comparison with it is false), as in the scan.  A row with no candidate (all -inf / NaN) yields 0.
-constexpr int SAMPLE_SPLIT = 32, SAMPLE_THREADS = 256;
-constexpr int NO_INDEX = 0x7fffffff;
+// Greedy / Gumbel-max token choice (cpu/sample.zig:17-45 semantics): one workgroup of ROW_THREADS lanes owns one
+// row and the whole choice is made in that workgroup, so no partial results leave it and no scratch is needed.
+// Every candidate (value v, index i) becomes one 64-bit key: the high word is v's bits mapped so that unsigned
+// order is float order, the low word is ~i.  The largest key is then the largest value and, among equal values,
+// the smallest index -- exactly what the reference's strictly-greater scan keeps -- so the reduction is a plain
+// unsigned max with no tie logic.  NaN and -inf never win that scan (no comparison with them is true), so they
+// are not candidates; key 0 means "no candidate" and yields index 0, the scan's starting index.
+// What bit parity with the CPU backend fixes is kept as it is: the splitmix64 stream per (seed, row, index), the
+// uniform from its top 24 bits and the Gumbel value v / t - log(-log u), each f32 operation rounded once.
+constexpr int ROW_THREADS = 1024;
 
-__device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
+__device__ __forceinline__ uint64_t mix64(uint64_t x) {  // SplitMix64 finaliser, as cpu/sample.zig:7-12
     x += 0x9E3779B97F4A7C15ull;
     x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
     x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
     return x ^ (x >> 31);
 }
 
-__device__ __forceinline__ void argmax_merge(float &bv, int &bi, float v, int i) {
-    if (v > bv || (v == bv && i < bi)) {
-        bv = v;
-        bi = i;
-    }
+__device__ __forceinline__ uint64_t cand_key(float v, int i) {
+    if (!(v > -INFINITY)) return 0;  // NaN, -inf
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)ord << 32) | (uint32_t)~(uint32_t)i;
 }
 
-__device__ __forceinline__ void wave_argmax(float &bv, int &bi) {
+__device__ __forceinline__ uint64_t shfl_xor64(uint64_t x, int m) {
+    const int lane = __lane_id();
+    const int lo = __builtin_amdgcn_ds_bpermute((lane ^ m) << 2, (int)(uint32_t)x);
+    const int hi = __builtin_amdgcn_ds_bpermute((lane ^ m) << 2, (int)(uint32_t)(x >> 32));
+    return ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
+}
+
+template <bool GUMBEL>
+__device__ __forceinline__ uint64_t scan_row(const bf16_t *row, int V, float temp, uint64_t rs) {
+    uint64_t best = 0;
+    auto take = [&](float x, int i) {
+        if (GUMBEL) {
+            const uint64_t r = mix64(rs + (uint64_t)i);
+            const float u = ((float)(r >> 40) + 0.5f) * (1.0f / 16777216.0f);
+            x = x / temp - logf(-logf(u));
+        }
+        const uint64_t k = cand_key(x, i);
+        best = k > best ? k : best;
+    };
+    // eight consecutive logits per lane per step: one 16-byte load when the row is 16-byte aligned
+    const bool vec = ((uintptr_t)row & 15) == 0;
+    for (int i0 = threadIdx.x * 8; i0 < V; i0 += ROW_THREADS * 8) {
+        if (vec && i0 + 8 <= V) {
+            float f[8];
+            unpack_bf16x8(ld16(row + i0), f);
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-        const float ov = lane_xor(bv, m);
-        const int oi = __builtin_bit_cast(int, lane_xor(__builtin_bit_cast(float, bi), m));
-        argmax_merge(bv, bi, ov, oi);
+            for (int e = 0; e < 8; ++e) take(f[e], i0 + e);
+        } else {
+            for (int i = i0; i < min(i0 + 8, V); ++i) take(bf2f(row[i]), i);
+        }
     }
+    return best;
 }
 
-__global__ void __launch_bounds__(SAMPLE_THREADS) sample_partial_kernel(float *pv, int *pi, const bf16_t *logits,
-                                                                        const float *temps, const uint64_t *seed,
-                                                                        int V) {
-    const int s = blockIdx.x, part = blockIdx.y;
-    const int chunk = (V + SAMPLE_SPLIT - 1) / SAMPLE_SPLIT;
-    const int beg = part * chunk, end = min(V, beg + chunk);
+__global__ void __launch_bounds__(ROW_THREADS) sample_rows_kernel(int *out, const bf16_t *logits, const float *temps,
+                                                                   const uint64_t *seed, int V) {
+    const int s = blockIdx.x;
     const bf16_t *row = logits + (long)s * V;
     const float temp = temps[s];
-    float bv = -INFINITY;
-    int bi = NO_INDEX;
-    if (temp > 0.0f) {
-        const uint64_t rs = splitmix64(*seed ^ ((uint64_t)s << 40));
-        for (int i = beg + threadIdx.x; i < end; i += SAMPLE_THREADS) {
-            const uint64_t r = splitmix64(rs + (uint64_t)i);
-            const float u = ((float)(r >> 40) + 0.5f) * (1.0f / 16777216.0f);
-            argmax_merge(bv, bi, bf2f(row[i]) / temp - logf(-logf(u)), i);
-        }
-    } else {
-        for (int i = beg + threadIdx.x; i < end; i += SAMPLE_THREADS) argmax_merge(bv, bi, bf2f(row[i]), i);
+    uint64_t best = temp > 0.0f ? scan_row<true>(row, V, temp, mix64(*seed ^ ((uint64_t)s << 40)))
+                                : scan_row<false>(row, V, temp, 0);
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+        const uint64_t o = shfl_xor64(best, m);
+        best = o > best ? o : best;
     }
-    wave_argmax(bv, bi);
-    __shared__ float sv[SAMPLE_THREADS / 64];
-    __shared__ int si[SAMPLE_THREADS / 64];
-    const int wave = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) {
-        sv[wave] = bv;
-        si[wave] = bi;
-    }
+    __shared__ uint64_t wave_best[ROW_THREADS / 64];
+    if ((threadIdx.x & 63) == 0) wave_best[threadIdx.x >> 6] = best;
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int w2 = 1; w2 < SAMPLE_THREADS / 64; ++w2) argmax_merge(bv, bi, sv[w2], si[w2]);
-        pv[s * SAMPLE_SPLIT + part] = bv;
-        pi[s * SAMPLE_SPLIT + part] = bi;
+        for (int w = 1; w < ROW_THREADS / 64; ++w) best = wave_best[w] > best ? wave_best[w] : best;
+        out[s] = best == 0 ? 0 : (int)~(uint32_t)best;
     }
-}
-
-__global__ void __launch_bounds__(64) sample_final_kernel(int *out, const float *pv, const int *pi) {
-    const int s = blockIdx.x, lane = threadIdx.x;
-    float bv = lane < SAMPLE_SPLIT ? pv[s * SAMPLE_SPLIT + lane] : -INFINITY;
-    int bi = lane < SAMPLE_SPLIT ? pi[s * SAMPLE_SPLIT + lane] : NO_INDEX;
-    wave_argmax(bv, bi);
-    if (lane == 0) out[s] = bi == NO_INDEX ? 0 : bi;
 }
 
 bool reject(const char *what) {
@@ -315,22 +321,22 @@ void hip_gather_rows(uint16_t *out, const uint16_t *x, const int32_t *idx, int S
     gather_rows_kernel<<<blocks_for(n, 256), 256, 0, g_llmgen_stream>>>(out, x, idx, S, H);
 }
 
+// The choice is made inside one workgroup per row: no scratch is needed (the argument stays for the reference's
+// argument list, sample.zig:4-14, and may be null).
 size_t hip_sample_scratch_bytes(int max_S) {
-    return max_S <= 0 ? 0 : (size_t)max_S * SAMPLE_SPLIT * (sizeof(float) + sizeof(int));
+    (void)max_S;
+    return 0;
 }
 
 void hip_sample(int32_t *out_ids, const uint16_t *logits, const float *temps, const uint64_t *seed, int S, int V,
                 void *scratch) {
+    (void)scratch;
     if (S <= 0) return;
-    if (V <= 0 || scratch == nullptr) {
-        reject("hip_sample: V must be positive and scratch non-null");
+    if (V <= 0) {
+        reject("hip_sample: V must be positive");
         return;
     }
-    float *pv = static_cast<float *>(scratch);
-    int *pi = reinterpret_cast<int *>(pv + (size_t)S * SAMPLE_SPLIT);
-    sample_partial_kernel<<<dim3(S, SAMPLE_SPLIT), SAMPLE_THREADS, 0, g_llmgen_stream>>>(pv, pi, logits, temps, seed,
-                                                                                         V);
-    sample_final_kernel<<<S, 64, 0, g_llmgen_stream>>>(out_ids, pv, pi);
+    sample_rows_kernel<<<S, ROW_THREADS, 0, g_llmgen_stream>>>(out_ids, logits, temps, seed, V);
 }
 
 }  // extern "C"

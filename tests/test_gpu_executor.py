@@ -110,3 +110,27 @@ def test_cpp_decode_graph_buckets(gpu):
             assert_cache_equal(to_u16(vc_g), to_u16(vc_e), f"graph V n={n}")
     finally:
         graphs.destroy()
+
+
+@pytest.mark.parametrize("name", ["c3", "c4", "c5d", "c5p"])
+def test_cpp_executor_full_configs_sampled_rows(gpu, name):
+    """The full-size configs through the C++ PagedAttentionImpl (llmgen_paged_attention), the entry non-Zig hosts
+    use: store_kv bit-exact over the whole cache, sampled rows (first and last of every tile and sequence plus
+    48 seeded random rows) against the oracle, and the C++ step bit-identical to the Python operator's."""
+    from harness import run_gpu
+    from test_gpu_attention import _sample_rows
+
+    wl = make(name)
+    wl.pad_rows = 0
+    print(f"[gpu-test] C++ executor {name}", flush=True)
+    t = wl.tensors(device="cuda")
+    seqs, entries = _seqs_entries(wl, np.random.default_rng(3))
+    out, kc, vc = _run_cpp(wl, t, seqs, entries, H.L().hip_attn_prefill_tile())
+    meta = wl.meta(64)
+    rows = _sample_rows(wl, meta)
+    okc, ovc, _, of = run_oracle(wl, t, rows=rows, threads=16)
+    assert_cache_equal(to_u16(kc), okc, f"{name} K")
+    assert_cache_equal(to_u16(vc), ovc, f"{name} V")
+    compare(to_u16(out)[rows], of, f"C++ {name}")
+    out_py, _, _ = run_gpu(wl, t)
+    np.testing.assert_array_equal(to_u16(out), to_u16(out_py))
