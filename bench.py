@@ -280,6 +280,7 @@ def main() -> int:
     # ---- the metric step: c2 decode (store_kv fused into split-K decode), replayed from a hipGraph bucket
     #      captured by the C++ executor slice (llmgen_graphs_*, the engine's captureGraphs / replay) ----
     from llmgen_amd import host as H
+    from llmgen_amd._lib import loaded_library
 
     st = Step("c2")
     wl = st.wl
@@ -342,6 +343,7 @@ def main() -> int:
                    "graph_ms": round(graph_ms, 4), "layers_per_graph": N_LAYERS,
                    "hbm_frac": round(value / HBM_PEAK_GBS, 4), "parallelism": "single GPU"},
         "roofline": roofline,
+        "library": loaded_library(),
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(st)

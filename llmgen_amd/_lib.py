@@ -67,6 +67,7 @@ SIGNATURES = {
 }
 
 _lib = None
+_lib_path = None
 
 
 class LibraryMissing(RuntimeError):
@@ -86,5 +87,17 @@ def lib() -> ctypes.CDLL:
         fn = getattr(handle, name)
         fn.restype = res
         fn.argtypes = args
-    _lib = handle
+    global _lib_path
+    _lib, _lib_path = handle, os.path.abspath(path)
     return handle
+
+
+def loaded_library() -> dict:
+    """Path and sha256 of the library this process loaded (recorded with every benchmark line)."""
+    import hashlib
+
+    lib()
+    with open(_lib_path, "rb") as f:
+        digest = hashlib.sha256(f.read()).hexdigest()
+    return {"path": os.path.relpath(_lib_path, os.path.dirname(os.path.dirname(os.path.abspath(__file__)))),
+            "sha256": digest}

@@ -157,7 +157,10 @@ def qwen_pair(gpu):
     from oracle.qwen3_ref import Qwen3Ref
 
     cfg = Qwen3Config()
-    W = random_weights(cfg, seed=1, embd_row_sigma=1.0)
+    # std 0.03, equal-norm embedding rows: the hidden state, not a few large embedding rows, decides the argmax,
+    # so the greedy ids change from step to step (with the log-normal row norms of embd_row_sigma > 0 a handful
+    # of rows win every step whatever attention returns)
+    W = random_weights(cfg, seed=GREEDY_SEED, std=0.03)
     num_blocks = 160
     gpu_model = Qwen3(cfg, W, num_blocks, max_seqs=4, max_tokens=256)
     tabs = rope_tables(cfg.max_model_len, cfg.head_dim, cfg.rope_theta)
@@ -171,8 +174,30 @@ def _logit_err(g: np.ndarray, c: np.ndarray):
     return float(np.abs(gf - cf).max()), float(np.linalg.norm(gf - cf) / np.linalg.norm(cf))
 
 
-@pytest.mark.timeout(600)
+GREEDY_SEED = 3
+DECISIVE = 4.0  # a row-step is decisive when its top-2 margin exceeds this many two-ordering drifts
+
+
+def _top2(lg_row: np.ndarray):
+    f = O.bf16_to_f32(lg_row).astype(np.float64)
+    i1 = int(np.argmax(f))
+    rest = f.copy()
+    rest[i1] = -np.inf
+    return f, i1, float(f[i1] - rest.max())
+
+
+@pytest.mark.timeout(900)
 def test_qwen3_greedy_ids_match_cpu_backend(qwen_pair):
+    """Greedy ids of the GPU forward against the CPU backend's, teacher-forced (both take the CPU's ids as the next
+    step's input), plus the logit bar.
+
+    A random 28-layer model turns one-ulp differences in attention outputs into ~2 % of the logits: the CPU
+    backend itself, with the reference's equally exact two-pass attention in place of its online one, drifts that
+    far.  So each row-step is judged against that floor, measured in the same run: where the CPU's top-2 margin
+    exceeds DECISIVE x the row's drift (rms of two-pass minus online logits), the GPU must pick the CPU's id;
+    elsewhere (a near tie) the GPU's pick must be within that band of the CPU's maximum.  The run must change ids
+    (at least 6 distinct over the run) and most row-steps must be decisive, so that an attention error that moved
+    the logits by more than the drift would change the ids."""
     cfg, G, C, C2 = qwen_pair
     mb = G.max_blocks
     rng = np.random.default_rng(5)
@@ -181,7 +206,8 @@ def test_qwen3_greedy_ids_match_cpu_backend(qwen_pair):
     prompts = [rng.integers(0, cfg.vocab, n).tolist() for n in lens]
     ents = [S.Entry(0, n, tables[i]) for i, n in enumerate(lens)]
     ids_in = sum(prompts, [])
-    gen_g, gen_c, errs, floors = [], [], [], []
+    gen_g, gen_c, errs, floors, margins = [], [], [], [], []
+    decisive = 0
     pos = list(lens)
     for step in range(7):
         meta = S.fill_meta(ents, cfg.block_size, mb, G.pf_tile)
@@ -189,18 +215,37 @@ def test_qwen3_greedy_ids_match_cpu_backend(qwen_pair):
         ids_g = G.forward(ents, ids_in, fused_qk=(step % 2 == 0))  # both pre-attention paths
         ids_c, lg_c = C.forward(meta, ids_in, mb, return_logits=True)
         _, lg_c2 = C2.forward(meta, ids_in, mb, return_logits=True)
-        errs.append(_logit_err(down(G.last_logits), lg_c))
+        lg_g = down(G.last_logits)
+        errs.append(_logit_err(lg_g, lg_c))
         floors.append(_logit_err(lg_c2, lg_c))
-        gen_g.append(list(ids_g))
+        gen_g.append([int(i) for i in ids_g])
         gen_c.append([int(i) for i in ids_c])
-        assert gen_g[-1] == gen_c[-1], f"step {step}: gpu {gen_g} cpu {gen_c}; logit err {errs} floor {floors}"
+        row_m = []
+        for r in range(len(lens)):
+            fc, ic, margin = _top2(lg_c[r])
+            drift = float(np.sqrt(np.mean((O.bf16_to_f32(lg_c2[r]).astype(np.float64) - fc) ** 2)))
+            row_m.append((round(margin, 4), round(drift, 4)))
+            assert ic == gen_c[-1][r]
+            if margin > DECISIVE * drift:
+                decisive += 1
+                assert gen_g[-1][r] == ic, (f"step {step} row {r}: gpu {gen_g[-1][r]} cpu {ic}, margin {margin:.4g} "
+                                            f"> {DECISIVE} x drift {drift:.4g}; logit err {errs[-1]}")
+            else:  # near tie: the GPU's pick must be one of the CPU's near-maximal logits
+                assert fc[gen_g[-1][r]] >= fc[ic] - DECISIVE * drift, (step, r, gen_g[-1][r], ic, margin, drift)
+        margins.append(row_m)
         ents = [S.Entry(pos[i], 1, tables[i]) for i in range(2)]
         ids_in = gen_c[-1]
         pos = [p + 1 for p in pos]
-    print(f"[qwen3] greedy ids {gen_c}")
+    print(f"[qwen3] greedy ids cpu {gen_c}")
+    print(f"[qwen3] greedy ids gpu {gen_g}")
+    print(f"[qwen3] (top-2 margin, two-ordering drift) per step and row: {margins}")
     print(f"[qwen3] logits vs CPU backend (max-abs, rel-L2) per step: {errs}")
     print(f"[qwen3] floor: two-pass CPU attention vs CPU backend: {floors}")
     check_err()
+    distinct = len({i for step in gen_c for i in step})
+    n_rows = 7 * len(lens)
+    assert distinct >= 6, f"ids barely change ({distinct} distinct): {gen_c}"
+    assert decisive >= n_rows * 2 // 3, f"only {decisive} of {n_rows} row-steps decisive: {margins}"
     for e, f in zip(errs, floors):
         assert e[1] <= 2 * f[1] + 1e-3, (errs, floors)
 
