@@ -61,6 +61,18 @@ void hip_attn_decode_store_kv(uint16_t *out, const uint16_t *q, const uint16_t *
                               int max_blocks, int block_size, float scale, float *part_o, float *part_ml,
                               int part_size, int max_parts);
 
+/* No reference counterpart.  hip_attn_decode for callers that cannot allocate or pass device memory (code under
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc): the split-K partials live in the
+ * library's own file-scope device array of 8 MiB per device instead of caller-owned part_o / part_ml, so the
+ * call allocates nothing.  Arguments and output as hip_attn_decode (part_size / max_parts as the engine computes
+ * them).  A launch whose partials need more than 8 MiB (S * nq * parts-per-sequence * 520 bytes, where the
+ * launcher keeps parts-per-sequence small: about 512 / (S * nkv) for long contexts, at least 1) prints one line
+ * and launches nothing.  All calls on one device share the array: calls that overlap on one device (two streams)
+ * race and must be serialised by the caller. */
+void hip_attn_decode_noalloc(uint16_t *out, const uint16_t *q, const uint16_t *k_cache, const uint16_t *v_cache,
+                             const int32_t *block_tables, const int32_t *ctx_lens, int S, int nq, int nkv, int hd,
+                             int max_blocks, int block_size, float scale, int part_size, int max_parts);
+
 /* Replaces cuda_attn_prefill (attention_v1.zig:30-47).  Causal varlen attention over the paged cache: sequence
  * s owns rows [cu_q[s], cu_q[s+1]) of q / out [T, nq, hd]; ctx_lens[s] = keys after this step; row j sits at
  * position ctx - q_len + j and attends to keys 0..pos.  Sequences with ctx < q_len are padding: rows of 0.

@@ -23,6 +23,7 @@ SIGNATURES = {
     "hip_attn_decode": (None, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P, _P, _I, _I]),
     "hip_attn_decode_store_kv": (None, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P, _P, _I,
                                         _I]),
+    "hip_attn_decode_noalloc": (None, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I, _I]),
     "hip_attn_prefill": (None, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F]),
     "hip_attn_prefill_rows": (None, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I]),
     "hip_attn_prefill_tile": (_I, []),

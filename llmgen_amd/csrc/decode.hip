@@ -574,10 +574,37 @@ void launch_decode_rows(dim3 grid, const DecodeArgs &a, int G) {
 }
 
 
+// Split-K scratch of hip_attn_decode_noalloc: a file-scope device array (each device holds its own copy for the
+// life of the process).  Host code never passes the array's name to a kernel: its device address is taken once
+// per device with hipGetSymbolAddress and kept here.  Every call on a device shares that device's array, so calls
+// that overlap on one device (two streams) race; the partials need no clearing (each slot is written before it
+// is read) and the merge counters reset themselves.
+constexpr size_t NOALLOC_SCRATCH_FLOATS = (size_t)2 << 20;  // 8 MiB
+__device__ __align__(256) float scratch[NOALLOC_SCRATCH_FLOATS];
+
+float *noalloc_scratch() {
+    static float *ptr[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    if (!ptr[dev]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            fprintf(stderr, "[llmgen-hip] attn_decode_noalloc: hipGetSymbolAddress failed: %s\n",
+                    hipGetErrorString(e));
+            return nullptr;
+        }
+        ptr[dev] = (float *)p;
+    }
+    return ptr[dev];
+}
+
+// own_scratch: part_o / part_ml are ignored and the partials go to the library's array above, packed with a
+// stride of the launch's own part count instead of max_parts.
 void decode_launch(bf16_t *out, const bf16_t *q, const bf16_t *k_new, const bf16_t *v_new, const int *slots,
                    bf16_t *k_cache, bf16_t *v_cache, const int *block_tables, const int *ctx_lens, int S, int nq,
                    int nkv, int hd, int max_blocks, int block_size, float scale, float *part_o, float *part_ml,
-                   int part_size, int max_parts) {
+                   int part_size, int max_parts, bool own_scratch = false) {
     if (S <= 0) return;
     if (hd != HD) {
         fprintf(stderr, "[llmgen-hip] attn_decode: only head_dim=128 is supported (got %d)\n", hd);
@@ -610,6 +637,21 @@ void decode_launch(bf16_t *out, const bf16_t *q, const bf16_t *k_new, const bf16
     const int k = std::max((int)(total > target ? total / target : 1), (round_tokens + part_size - 1) / part_size);
     const int nparts = (max_parts + k - 1) / k;
     int stride = max_parts;  // partial slots per (sequence, head) in part_o / part_ml
+    if (own_scratch) {
+        const size_t rows = (size_t)S * nq * nparts;
+        if (rows * (HD + 2) > NOALLOC_SCRATCH_FLOATS) {
+            fprintf(stderr,
+                    "[llmgen-hip] attn_decode_noalloc: this launch needs %zu bytes of split-K scratch, more than the "
+                    "library's %zu; use hip_attn_decode with caller-owned scratch\n",
+                    rows * (HD + 2) * sizeof(float), NOALLOC_SCRATCH_FLOATS * sizeof(float));
+            return;
+        }
+        float *base = noalloc_scratch();
+        if (!base) return;
+        part_o = base;
+        part_ml = base + rows * HD;
+        stride = nparts;
+    }
     int *counters = (long)S * nkv <= MAX_MERGE_SEGMENTS && !llmgen_opt(LLMGEN_OPT_DECODE_MERGE_KERNEL)
                         ? merge_counters()
                         : nullptr;
@@ -637,6 +679,16 @@ extern "C" void hip_attn_decode(bf16_t *out, const bf16_t *q, const bf16_t *k_ca
     decode_launch(out, q, nullptr, nullptr, nullptr, const_cast<bf16_t *>(k_cache), const_cast<bf16_t *>(v_cache),
                   block_tables, ctx_lens, S, nq, nkv, hd, max_blocks, block_size, scale, part_o, part_ml, part_size,
                   max_parts);
+}
+
+// hip_attn_decode with the split-K partials in the library's own device array: allocates nothing, takes no
+// scratch from the caller.
+extern "C" void hip_attn_decode_noalloc(bf16_t *out, const bf16_t *q, const bf16_t *k_cache, const bf16_t *v_cache,
+                                        const int *block_tables, const int *ctx_lens, int S, int nq, int nkv, int hd,
+                                        int max_blocks, int block_size, float scale, int part_size, int max_parts) {
+    decode_launch(out, q, nullptr, nullptr, nullptr, const_cast<bf16_t *>(k_cache), const_cast<bf16_t *>(v_cache),
+                  block_tables, ctx_lens, S, nq, nkv, hd, max_blocks, block_size, scale, nullptr, nullptr, part_size,
+                  max_parts, true);
 }
 
 // store_kv of the step's one token per sequence fused into the decode launch (one kernel instead of two).

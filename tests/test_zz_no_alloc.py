@@ -1,0 +1,71 @@
+"""GPU: hip_attn_decode_noalloc (split-K partials in the library's own device array, no caller scratch, no
+allocation) gives bit for bit what hip_attn_decode gives with caller-owned scratch, on consecutive calls whose
+inputs shrink (so the second call finds the first call's partials in the shared array), and rejects a launch
+whose partials exceed the array without launching anything."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from harness import check_hip_error
+from llmgen_amd import step as S
+from llmgen_amd._lib import lib
+from llmgen_amd.workloads import make, to_u16
+
+pytestmark = pytest.mark.gpu
+
+
+def _decode_inputs(name, n_seq=None):
+    wl = make(name)
+    if n_seq is not None:
+        wl.entries = wl.entries[:n_seq]
+    t = wl.tensors(device="cuda")
+    meta = wl.meta(64)
+    assert meta.decode
+    n = meta.n_tok
+    d = lambda a: torch.from_numpy(a).to("cuda")  # noqa: E731
+    kc, vc = t["kc"].clone(), t["vc"].clone()
+    lib().hip_store_kv(t["k"].data_ptr(), t["v"].data_ptr(), d(meta.slots).data_ptr(), kc.data_ptr(),
+                       vc.data_ptr(), n, wl.nkv, wl.hd, wl.block_size)
+    return wl, n, t["q"][:n].contiguous(), kc, vc, d(meta.block_tables), d(meta.ctx)
+
+
+def _both(wl, n, q, kc, vc, bt, ctx):
+    L = lib()
+    ps, mp = S.part_size(n), S.max_parts(n, wl.max_model_len)
+    common = (q.data_ptr(), kc.data_ptr(), vc.data_ptr(), bt.data_ptr(), ctx.data_ptr(), n, wl.nq, wl.nkv, wl.hd,
+              wl.max_blocks, wl.block_size, wl.scale)
+    po = torch.empty(n * wl.nq * mp * wl.hd, dtype=torch.float32, device="cuda")
+    pml = torch.empty(n * wl.nq * mp * 2, dtype=torch.float32, device="cuda")
+    ref = torch.full((n, wl.nq, wl.hd), float("nan"), dtype=torch.bfloat16, device="cuda")
+    L.hip_attn_decode(ref.data_ptr(), *common, po.data_ptr(), pml.data_ptr(), ps, mp)
+    got = torch.full_like(ref, float("nan"))
+    L.hip_attn_decode_noalloc(got.data_ptr(), *common, ps, mp)
+    torch.cuda.synchronize()
+    check_hip_error(f"noalloc {wl.name}")
+    return to_u16(ref), to_u16(got)
+
+
+def test_noalloc_decode_equals_caller_scratch_on_shrinking_calls(gpu):
+    # c5d: 16 x 32K keys, split into several partials per (sequence, head); then smaller launches that reuse
+    # the same array: c1 (1 sequence, 4-wave workgroups, partials merged in the kernel), kt_decode, c2 subset
+    for name, n_seq in (("c5d", None), ("c1", None), ("kt_decode", None), ("c2", 20)):
+        print(f"[gpu-test] noalloc {name} n_seq={n_seq}", flush=True)
+        ref, got = _both(*_decode_inputs(name, n_seq))
+        assert np.isfinite(ref.view(np.int16).astype(np.float32)).all()
+        np.testing.assert_array_equal(got, ref, err_msg=f"noalloc != hip_attn_decode on {name}")
+
+
+def test_noalloc_decode_rejects_oversized_launch(gpu):
+    """A launch whose partials would need more than the array (20000 sequences, 16 heads) prints one line and
+    launches nothing: the output is untouched and no HIP error is raised."""
+    print("[gpu-test] noalloc oversized", flush=True)
+    out = torch.full((4, 16, 128), 3.0, dtype=torch.bfloat16, device="cuda")
+    before = to_u16(out).copy()
+    dummy = torch.zeros(1 << 12, dtype=torch.int32, device="cuda").data_ptr()
+    lib().hip_attn_decode_noalloc(out.data_ptr(), dummy, dummy, dummy, dummy, dummy, 20000, 16, 8, 128, 64, 256,
+                                  0.088, 512, 64)
+    torch.cuda.synchronize()
+    check_hip_error("noalloc oversized")
+    np.testing.assert_array_equal(to_u16(out), before)

@@ -71,6 +71,24 @@ pub extern fn hip_attn_decode_store_kv(
     max_parts: c_int,
 ) void;
 
+pub extern fn hip_attn_decode_noalloc(
+    out: ?*anyopaque,
+    q: ?*const anyopaque,
+    k_cache: ?*const anyopaque,
+    v_cache: ?*const anyopaque,
+    block_tables: ?*const anyopaque,
+    ctx_lens: ?*const anyopaque,
+    S: c_int,
+    nq: c_int,
+    nkv: c_int,
+    hd: c_int,
+    max_blocks: c_int,
+    block_size: c_int,
+    scale: f32,
+    part_size: c_int,
+    max_parts: c_int,
+) void;
+
 pub extern fn hip_attn_prefill(
     out: ?*anyopaque,
     q: ?*const anyopaque,
