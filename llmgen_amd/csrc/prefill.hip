@@ -82,8 +82,11 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const bf16_t *base, 
     return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, bytes, BUF_WORD3);
 }
 
-// NW = waves per workgroup (2 per head: rows 0-31 and 32-63 of the tile); MODE = DmaMode.
-template <int NW, int MODE>
+// NW = waves per workgroup; MODE = DmaMode; KS = key groups.  The waves form KS key groups of NW / KS waves, two
+// per head (rows 0-31 and 32-63 of the tile).  With KS = 2 group k takes the key tiles k, k + 2, k + 4, ... into
+// its own LDS stages, so a unit of n key tiles takes ceil(n / 2) iterations; the two groups' (m, l, O) are merged
+// through LDS at the end in a fixed order (bit-reproducible, and a tile's keys always go to the same group).
+template <int NW, int MODE, int KS>
 __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)))
     attn_prefill_kernel(bf16_t *__restrict__ out, const bf16_t *__restrict__ q, const bf16_t *__restrict__ kc,
                         const bf16_t *__restrict__ vc, const int *__restrict__ block_tables,
@@ -91,14 +94,16 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
                         const int *__restrict__ tile_seq, const int *__restrict__ tile_q0, int n_tiles, int nq,
                         int nkv, int G, int head_groups, int max_blocks, int block_size, int bs_shift,
                         float scale_log2) {
-    constexpr int LOADS = 16 / NW;  // 4-row DMA instructions per wave per tile, for K and for V each
+    constexpr int NWG = NW / KS;     // waves per key group
+    constexpr int LOADS = 16 / NWG;  // 4-row DMA instructions per wave per tile, for K and for V each
 
-    __shared__ __attribute__((aligned(16))) bf16_t K0[TILE];
-    __shared__ __attribute__((aligned(16))) bf16_t V0[TILE];
+    // stage buffers: one 64-key K and V tile per key group
+    __shared__ __attribute__((aligned(16))) bf16_t K0[KS * TILE];
+    __shared__ __attribute__((aligned(16))) bf16_t V0[KS * TILE];
     // 2-wave workgroups (G = 1) keep one stage: 32 KB of LDS lets four of them share a CU (two waves per SIMD)
     constexpr bool ONE_STAGE = NW == 2;
-    __shared__ __attribute__((aligned(16))) bf16_t K1[ONE_STAGE ? 8 : TILE];
-    __shared__ __attribute__((aligned(16))) bf16_t V1[ONE_STAGE ? 8 : TILE];
+    __shared__ __attribute__((aligned(16))) bf16_t K1[ONE_STAGE ? 8 : KS * TILE];
+    __shared__ __attribute__((aligned(16))) bf16_t V1[ONE_STAGE ? 8 : KS * TILE];
 
     const int bid = blockIdx.x;
     const int kvh = bid % nkv;
@@ -108,9 +113,10 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
     const int s = tile_seq[tile], q0 = tile_q0[tile];
     const int q_beg = cu_q[s], q_len = cu_q[s + 1] - q_beg, ctx = ctx_lens[s];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int g = hg * (NW / 2) + (wave >> 1);  // head within the KV group
+    const int kg = wave / NWG, wl = wave % NWG;  // key group, wave within the group
+    const int g = hg * (NWG / 2) + (wl >> 1);    // head within the KV group
     const int head = kvh * G + g;
-    const int r0 = q0 + (wave & 1) * 32;  // first query row (within the segment) of this wave
+    const int r0 = q0 + (wl & 1) * 32;  // first query row (within the segment) of this wave
     const int l32 = lane & 31, hh = lane >> 5;
 
     if (q_len == 1) return;  // single-row segments (decode rows of a mixed step): streamed by the decode kernel
@@ -128,7 +134,8 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
     const long head_off = (long)kvh * block_size * HD;
     const int base_pos = ctx - q_len;                // position of segment row 0
     const int kend = base_pos + min(q0 + BQ, q_len);  // keys needed by the whole tile
-    const int n_iter = (kend + BK - 1) / BK;
+    const int n_iter = (kend + BK - 1) / BK;  // key tiles
+    const int n_super = (n_iter + KS - 1) / KS;  // iterations: one tile per key group each
 
     // ---- Q fragments (B operand): lane holds row r0+l32, dims c*16 + hh*8 .. +8 ----
     const int my_row = r0 + l32;
@@ -146,11 +153,16 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
     const int wave_pos_max = base_pos + min(r0 + 31, q_len - 1);
     const bool wave_has_pad = r0 + 31 >= q_len;
 
-    // ---- DMA of one K/V tile into (Kd, Vd): wave instruction i covers rows 4*(wave + NW*i) .. +3; lane writes
-    //      row + lane/16, physical chunk lane%16, so it reads the logical chunk that swizzles onto it ----
+    // ---- DMA of this group's K/V tile of iteration `it` into (Kd, Vd): wave instruction i covers rows
+    //      4*(wl + NWG*i) .. +3; lane writes row + lane/16, physical chunk lane%16, so it reads the logical chunk
+    //      that swizzles onto it ----
     const int drow = lane >> 4, dchunk = lane & 15;
     auto issue = [&](int it, bf16_t *Kd, bf16_t *Vd) {
-        const int kb0 = it * BK;
+        const int ti = it * KS + kg;
+        if (KS > 1 && ti >= n_iter) return;  // the unit's last iteration has no tile for this group
+        Kd += kg * TILE;
+        Vd += kg * TILE;
+        const int kb0 = ti * BK;
         const int last = kend - 1 - kb0;  // keys past kend reread the last valid key (finite data)
         __amdgpu_buffer_rsrc_t krs, vrs;
         if (MODE == DMA_BLOCK) {  // the whole tile lies in one block: one descriptor pair per tile
@@ -161,7 +173,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
         }
 #pragma unroll
         for (int i = 0; i < LOADS; ++i) {
-            const int rbase = 4 * (wave + NW * i);
+            const int rbase = 4 * (wl + NWG * i);
             const int r = rbase + drow;
             const int kswz = (dchunk ^ (r & 15)) << 4, vswz = (dchunk ^ ((r << 2) & 15)) << 4;  // bytes
             if (MODE == DMA_BLOCK) {
@@ -326,8 +338,11 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
         }
     };
     auto compute = [&](int it, const bf16_t *Ks, const bf16_t *Vs) {
-        const int kb0 = it * BK;
-        if (wave_active && kb0 <= wave_pos_max) {
+        const int ti = it * KS + kg;
+        const int kb0 = ti * BK;
+        Ks += kg * TILE;
+        Vs += kg * TILE;
+        if (wave_active && ti < n_iter && kb0 <= wave_pos_max) {
             // tiles wholly below the wave's diagonal (and with no padding rows) take the unmasked path
             if (wave_has_pad || kb0 + BK - 1 > wave_pos_min)
                 tile_step(kb0, Ks, Vs, std::true_type{});
@@ -339,7 +354,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
     // two LDS stages; the loop is unrolled twice so every DMA targets a fixed buffer (the compiler can then see
     // that the reads of one stage never wait for the DMA into the other)
     if (ONE_STAGE) {
-        for (int it = 0; it < n_iter; ++it) {
+        for (int it = 0; it < n_super; ++it) {
             issue(it, K0, V0);
             __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();  // the tile has landed for every wave
@@ -347,20 +362,47 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
             __syncthreads();  // every wave is done reading it
         }
     } else {
-        if (n_iter > 0) issue(0, K0, V0);
+        if (n_super > 0) issue(0, K0, V0);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        for (int it = 0; it < n_iter; it += 2) {
-            if (it + 1 < n_iter) issue(it + 1, K1, V1);
+        for (int it = 0; it < n_super; it += 2) {
+            if (it + 1 < n_super) issue(it + 1, K1, V1);
             compute(it, K0, V0);
             __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA into stage 1 has landed
             __syncthreads();                // ... and everyone's; everyone is done reading stage 0
-            if (it + 1 >= n_iter) break;
-            if (it + 2 < n_iter) issue(it + 2, K0, V0);
+            if (it + 1 >= n_super) break;
+            if (it + 2 < n_super) issue(it + 2, K0, V0);
             compute(it + 1, K1, V1);
             __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
         }
+    }
+
+    if constexpr (KS == 2) {
+        // ---- merge the key groups: group 1 leaves (o, m, l) in LDS (the stage buffers are free: the loop ended
+        //      on a barrier), group 0 combines them with its own, lane by lane (both groups hold the same rows in
+        //      the same accumulator layout, and m is equal across a row's two half-waves) ----
+        float *xo = reinterpret_cast<float *>(wl < 2 ? K0 : V0) + (wl & 1) * 64 * 64;  // [64 values][64 lanes]
+        float *xm = reinterpret_cast<float *>(K1) + wl * 2 * 64;                       // [m, l][64 lanes]
+        if (kg == 1) {
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) xo[(db * 16 + r) * 64 + lane] = o[db][r];
+            xm[lane] = m_run;
+            xm[64 + lane] = l_run;
+        }
+        __syncthreads();
+        if (kg == 1) return;
+        const float m1 = xm[lane], l1 = xm[64 + lane];
+        const float M = fmaxf(m_run, m1);
+        const float Mu = M == -INFINITY ? 0.f : M;
+        const float c0 = fast_exp2(m_run - Mu), c1 = fast_exp2(m1 - Mu);
+        l_run = l_run * c0 + l1 * c1;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[db][r] = o[db][r] * c0 + xo[(db * 16 + r) * 64 + lane] * c1;
     }
 
     // ---- normalise and store: lane holds dims db*32 + (r/4)*8 + hh*4 + r%4 of row my_row ----
@@ -380,22 +422,22 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
         }
 }
 
-template <int NW, int MODE>
+template <int NW, int MODE, int KS>
 void launch_prefill_mode(long grid, bf16_t *out, const bf16_t *q, const bf16_t *kc, const bf16_t *vc, const int *bt,
                          const int *ctx, const int *cu_q, const int *tile_seq, const int *tile_q0, int n_tiles, int nq,
                          int nkv, int G, int head_groups, int max_blocks, int block_size, int bs_shift, float sl2) {
-    hipLaunchKernelGGL((attn_prefill_kernel<NW, MODE>), dim3((unsigned)grid), dim3(64 * NW), 0, g_llmgen_stream, out, q,
+    hipLaunchKernelGGL((attn_prefill_kernel<NW, MODE, KS>), dim3((unsigned)grid), dim3(64 * NW), 0, g_llmgen_stream, out, q,
                        kc, vc, bt, ctx, cu_q, tile_seq, tile_q0, n_tiles, nq, nkv, G, head_groups, max_blocks,
                        block_size, bs_shift, sl2);
 }
 
-template <int NW>
+template <int NW, int KS = 1>
 void launch_prefill(int mode, int head_groups, bf16_t *out, const bf16_t *q, const bf16_t *kc, const bf16_t *vc,
                     const int *bt, const int *ctx, const int *cu_q, const int *tile_seq, const int *tile_q0,
                     int n_tiles, int nq, int nkv, int G, int max_blocks, int block_size, int bs_shift, float sl2) {
     const long grid = (long)n_tiles * nkv * head_groups;
     auto go = [&](auto m) {
-        launch_prefill_mode<NW, decltype(m)::value>(grid, out, q, kc, vc, bt, ctx, cu_q, tile_seq, tile_q0, n_tiles,
+        launch_prefill_mode<NW, decltype(m)::value, KS>(grid, out, q, kc, vc, bt, ctx, cu_q, tile_seq, tile_q0, n_tiles,
                                                     nq, nkv, G, head_groups, max_blocks, block_size, bs_shift, sl2);
     };
     if (mode == DMA_BLOCK) go(std::integral_constant<int, DMA_BLOCK>{});
@@ -445,8 +487,18 @@ extern "C" void hip_attn_prefill_rows(bf16_t *out, const bf16_t *q, const bf16_t
     switch (heads_per_wg) {
         case 1: launch_prefill<2>(mode, head_groups, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq,
                                   tile_q0, n_tiles, nq, nkv, G, max_blocks, block_size, bs_shift, sl2); break;
-        case 2: launch_prefill<4>(mode, head_groups, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq,
-                                  tile_q0, n_tiles, nq, nkv, G, max_blocks, block_size, bs_shift, sl2); break;
+        case 2:
+            // Pure prefill: 8-wave workgroups whose two key groups split each unit's key tiles, so the heaviest
+            // units (the long prompt's last tiles) take half as many iterations (c3 -7 %).  With decode rows beside
+            // it (single_rows != 0) a 128 KB workgroup finds no room next to the decode kernel's waves, and 4-wave
+            // workgroups (two per CU) are faster (c4 +9 % otherwise).
+            if (single_rows == 0)
+                launch_prefill<8, 2>(mode, head_groups, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q,
+                                     tile_seq, tile_q0, n_tiles, nq, nkv, G, max_blocks, block_size, bs_shift, sl2);
+            else
+                launch_prefill<4>(mode, head_groups, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q,
+                                  tile_seq, tile_q0, n_tiles, nq, nkv, G, max_blocks, block_size, bs_shift, sl2);
+            break;
         default: launch_prefill<8>(mode, head_groups, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq,
                                    tile_q0, n_tiles, nq, nkv, G, max_blocks, block_size, bs_shift, sl2); break;
     }
