@@ -84,7 +84,10 @@ def lib() -> ctypes.CDLL:
     if not os.path.exists(path):
         raise LibraryMissing(f"{path} is not built; run `python -m llmgen_amd.build` (hipcc, gfx950)")
     handle = ctypes.CDLL(path)
+    alt = "LLMGEN_ATTN_LIB" in os.environ  # an A/B build may predate some entry points: bind what it has
     for name, (res, args) in SIGNATURES.items():
+        if alt and not hasattr(handle, name):
+            continue
         fn = getattr(handle, name)
         fn.restype = res
         fn.argtypes = args

@@ -435,6 +435,9 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(3))
     if (tid == 0) s_last = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == np - 1;
     __syncthreads();
     if (!s_last) return;
+    // acquire at agent scope: the other workgroups' partials, published before their ticket increments, are read
+    // after this point (the loads below are agent-scope atomics as well)
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     for (int idx = tid; idx < G * HD; idx += NTH) {
         const int g = idx / HD, d = idx % HD;
         const long h = (long)kvh * G + g;
