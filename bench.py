@@ -64,12 +64,15 @@ def time_launches(fn, iters: int, warmup: int) -> float:
     return ms / iters
 
 
-def warm(fn, seconds: float = 0.5) -> None:
+WARM_S = 0.5
+
+
+def warm(fn, seconds: float = None) -> None:
     """Run fn() back to back for about ``seconds``: the GPU's clocks rise and every rotating pool copy has been
     touched once (its pages mapped) before anything is timed."""
     import torch
 
-    t_end = time.perf_counter() + seconds
+    t_end = time.perf_counter() + (WARM_S if seconds is None else seconds)
     while time.perf_counter() < t_end:
         for _ in range(20):
             fn()
@@ -254,12 +257,16 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warm-s", type=float, default=0.5,
+                    help="seconds of untimed launches before each timed loop (clocks up, pool copies touched)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--only", default=None, help="time only this config's attention launcher (for profiling)")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="run only a plain device copy of this many MiB (calibrates rocprofv3 FETCH/WRITE_SIZE)")
     args = ap.parse_args()
+    global WARM_S
+    WARM_S = args.warm_s
 
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (the attention kernel on one GPU's share); "
