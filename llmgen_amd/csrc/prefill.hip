@@ -112,13 +112,14 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
     const int tile = n_tiles - 1 - rest / head_groups;
     const int s = tile_seq[tile], q0 = tile_q0[tile];
     const int q_beg = cu_q[s], q_len = cu_q[s + 1] - q_beg, ctx = ctx_lens[s];
-    // Key-split kernels take the wave index through readfirstlane, so that the key-tile index derived from it, and
-    // with it the DMA descriptors, stay in scalar registers (otherwise each DMA is wrapped in a loop over distinct
-    // descriptor values).  The single-group kernels have a key-tile index without wave terms and measure faster
-    // with the plain index (c5p 2104 against 1931 us, c4 238 against 235 us): only the compiler's schedule differs.
+    // The key group is taken through readfirstlane (it is uniform across the wave), so that the key-tile index
+    // derived from it, and with it the DMA descriptors, stay in scalar registers; otherwise each DMA is wrapped in a
+    // loop over distinct descriptor values.  The wave index itself stays a plain vector value: taking it through
+    // readfirstlane as well measures slower (c5p 2104 against 1931 us, c3 85.6 against 82.2 us; only the
+    // compiler's schedule differs).
     const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = KS == 1 ? (tid >> 6) : __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int kg = KS == 1 ? 0 : wave / NWG, wl = wave % NWG;  // key group, wave within the group
+    const int wave = tid >> 6;
+    const int kg = KS == 1 ? 0 : __builtin_amdgcn_readfirstlane(wave) / NWG, wl = wave % NWG;
     const int g = hg * (NWG / 2) + (wl >> 1);    // head within the KV group
     const int head = kvh * G + g;
     const int r0 = q0 + (wl & 1) * 32;  // first query row (within the segment) of this wave

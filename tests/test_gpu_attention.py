@@ -299,6 +299,32 @@ def test_c5p_chunked_prefill_equals_tail(gpu):
     np.testing.assert_array_equal(to_u16(out_chunk), to_u16(out_full)[L - tail:])
 
 
+@pytest.mark.parametrize("tail", [1024, 1000])
+def test_c3_chunked_prefill_equals_tail(gpu, tail):
+    """c3's 3584-token prompt alone (GQA 2, a pure prefill step: the key-split kernel), then its last `tail` tokens
+    as a chunk against the cached rest: bit-identical to the tail of the full prefill.  Key tiles sit at absolute
+    positions, so each tile goes to the same key group in both runs and every row sums the same keys in the same
+    order; 1000 is not a multiple of the 64-row tile, so the chunk's tiles start mid-tile of the full prefill."""
+    import copy as _copy
+
+    from llmgen_amd.step import Entry
+
+    wl = _copy.copy(make("c3"))
+    wl.entries = wl.entries[:1]
+    L = wl.entries[0].q_len
+    print(f"[gpu-test] c3 chunk tail={tail}", flush=True)
+    t = wl.tensors(device="cuda")
+    t = {k: (v[:L].contiguous() if k in ("q", "k", "v") else v) for k, v in t.items()}
+    assert wl.meta(lib().hip_attn_prefill_tile()).single_rows() == 0
+    out_full, kc, vc = _step(wl, t)
+    wl2 = _copy.copy(wl)
+    wl2.entries = [Entry(L - tail, tail, wl.entries[0].block_table)]
+    t2 = {"q": t["q"][L - tail:].contiguous(), "k": t["k"][L - tail:].contiguous(),
+          "v": t["v"][L - tail:].contiguous(), "kc": kc, "vc": vc}
+    out_chunk, _, _ = _step(wl2, t2)
+    np.testing.assert_array_equal(to_u16(out_chunk), to_u16(out_full)[L - tail:])
+
+
 def test_zero_sized_launches_are_noops(gpu):
     """T <= 0, S <= 0 and n_tiles <= 0 launch nothing (the reference's degenerate-input contract), also for the
     fused entry points; the output buffer is untouched and no error is raised."""
