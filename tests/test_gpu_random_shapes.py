@@ -50,6 +50,43 @@ def _random_workload(case: int) -> Workload:
                     note=f"random: G={G} nkv={nkv} bs={bs} S={S} {'decode' if decode_only else 'mixed'}")
 
 
+PREFILL_CASES = list(range(8))
+
+
+def _random_prefill_workload(case: int) -> Workload:
+    """Pure prefill steps (fresh prompts and chunked tails, no decode rows) at GQA 2: the key-split kernel's path.
+    Prompt lengths cross 1, 2 and many key tiles, odd and even tile counts, and tiles that straddle blocks."""
+    rng = np.random.default_rng(2000 + case)
+    nkv = int(rng.choice([1, 2, 4, 8]))
+    bs = int(rng.choice([6, 16, 48, 64, 256]))
+    S = int(rng.integers(1, 7))
+    spec = []
+    for _ in range(S):
+        q = int(rng.integers(2, 700))
+        prev = 0 if rng.integers(0, 2) == 0 else int(rng.integers(1, 900))
+        spec.append((prev, q))
+    ctxs = [a + b for a, b in spec]
+    tables, nb = _tables(rng, ctxs, bs, permute=True, extra_blocks=2)
+    mb = max(len(t) for t in tables)
+    ents = [Entry(a, b, t) for (a, b), t in zip(spec, tables)]
+    return Workload(f"rprefill{case}", 2 * nkv, nkv, 128, bs, nb, mb, mb * bs, ents, std=1.0, seed=80 + case,
+                    decode=False, note=f"random prefill: G=2 nkv={nkv} bs={bs} S={S}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", PREFILL_CASES)
+def test_random_gqa2_prefill_matches_oracle(gpu, case):
+    wl = _random_prefill_workload(case)
+    print(f"[gpu-test] {wl.name}: {wl.note}", flush=True)
+    assert wl.meta(64).single_rows() == 0  # a pure prefill step: the key-split kernel runs
+    t = wl.tensors(device="cuda")
+    out, kc, vc = run_gpu(wl, t)
+    okc, ovc, _, of = run_oracle(wl, t, threads=16)
+    assert_cache_equal(to_u16(kc), okc, f"{wl.name} store_kv K")
+    assert_cache_equal(to_u16(vc), ovc, f"{wl.name} store_kv V")
+    compare(to_u16(out), of, wl.name)
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("case", CASES)
 def test_random_step_matches_oracle(gpu, case):
@@ -75,3 +112,10 @@ def test_random_shapes_are_valid():
         seen_bs.add(wl.block_size)
         kinds.add(wl.decode is None)
     assert len(seen_g) >= 3 and len(seen_bs) >= 3 and kinds == {True, False}
+    bss = set()
+    for case in PREFILL_CASES:
+        wl = _random_prefill_workload(case)
+        meta = wl.meta(64)
+        assert meta.single_rows() == 0 and not meta.decode
+        bss.add(wl.block_size)
+    assert len(bss) >= 3
