@@ -626,6 +626,11 @@ void decode_launch(bf16_t *out, const bf16_t *q, const bf16_t *k_new, const bf16
     // SV_ATTN_PART (attention.cu:219-229): parts only ever get longer, so max_parts slots still suffice
     const int part_min = llmgen_opt(LLMGEN_OPT_ATTN_PART_MIN);
     if (part_min > part_size) part_size = part_min;
+    if ((long)part_size * max_parts > 0x7fffffffL) {  // token positions are int32 throughout
+        fprintf(stderr, "[llmgen-hip] attn_decode: part_size * max_parts (%d * %d) exceeds the int32 token range\n",
+                part_size, max_parts);
+        return;
+    }
     // Each workgroup takes k consecutive parts (span = k * part_size tokens, one partial result).  k grows
     // with the launch so that a long-context launch has about 8 waves per compute unit (two 4-wave or one
     // 8-wave workgroup), each streaming a long span, instead of many short workgroups; partial slots stay
@@ -637,8 +642,10 @@ void decode_launch(bf16_t *out, const bf16_t *q, const bf16_t *k_new, const bf16
     // ... and a span is at least one round (W waves x 32 tokens, 16 at G = 16), so that no wave of a workgroup
     // idles: small batches have 64-token parts (c1: 9.4 -> 8.0 us)
     const int round_tokens = W * (G >= 16 ? 16 : 32);
-    const int k = std::max((int)(total > target ? total / target : 1), (round_tokens + part_size - 1) / part_size);
+    const int k = std::max((int)(total > target ? total / target : 1),
+                           (int)(((long)round_tokens + part_size - 1) / part_size));
     const int nparts = (max_parts + k - 1) / k;
+    const int span = (int)std::min((long)part_size * k, 1L << 30);  // tokens per workgroup (no int overflow)
     int stride = max_parts;  // partial slots per (sequence, head) in part_o / part_ml
     if (own_scratch) {
         const size_t rows = (size_t)S * nq * nparts;
@@ -660,7 +667,7 @@ void decode_launch(bf16_t *out, const bf16_t *q, const bf16_t *k_new, const bf16
                         : nullptr;
     DecodeArgs a{out, q, k_cache, v_cache, block_tables, ctx_lens, nq, nkv, max_blocks, block_size,
                  (block_size & (block_size - 1)) == 0 ? __builtin_ctz(block_size) : -1, scale * LLMGEN_LOG2E,
-                 part_o, part_ml, part_size * k, stride, nparts, counters};
+                 part_o, part_ml, span, stride, nparts, counters};
     a.k_new = k_new;
     a.v_new = v_new;
     a.slots = slots;

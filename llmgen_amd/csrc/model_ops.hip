@@ -185,6 +185,7 @@ __device__ __forceinline__ uint64_t mix64(uint64_t x) {  // SplitMix64 finaliser
 
 __device__ __forceinline__ uint64_t cand_key(float v, int i) {
     if (!(v > -INFINITY)) return 0;  // NaN, -inf
+    if (v == 0.f) v = 0.f;           // -0 == +0 for the scan: equal keys, so the smaller index wins
     const uint32_t u = __builtin_bit_cast(uint32_t, v);
     const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
     return ((uint64_t)ord << 32) | (uint32_t)~(uint32_t)i;

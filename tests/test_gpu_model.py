@@ -132,9 +132,12 @@ def test_sample_greedy_and_gumbel(gpu):
     lg[3, 9] = np.nan
     lg[3, 10] = 31.0
     lg[4, V - 1] = 40.0  # maximum in the last chunk
+    lg[5, :] = -1.0  # maximum 0, first as -0 then as +0: equal values, the first index wins
     b = O.f32_to_bf16(lg)
     b[2, :] = 0xFF80  # -inf in bf16
     b[3, 9] = 0x7FC0
+    b[5, 300] = 0x8000  # -0
+    b[5, 7000] = 0x0000  # +0
     L = lib()
     scratch = torch.empty(L.hip_sample_scratch_bytes(S_), dtype=torch.uint8, device=gpu)
     out = torch.empty(S_, dtype=torch.int32, device=gpu)
@@ -148,6 +151,10 @@ def test_sample_greedy_and_gumbel(gpu):
         ref = O.sample(b, temps, seed=987654321)
         np.testing.assert_array_equal(got, ref)
     assert list(got[1:5]) == [77, 0, 10, V - 1]
+    L.hip_sample(out.data_ptr(), ld.data_ptr(), up(np.zeros(S_, np.float32)).data_ptr(), seed.data_ptr(), S_, V,
+                 scratch.data_ptr())
+    check_err()
+    assert down(out)[5] == 300 and O.sample(b, np.zeros(S_, np.float32))[5] == 300
 
 
 # ---------------------------------------------------------------- the whole model
