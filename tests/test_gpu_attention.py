@@ -497,3 +497,43 @@ def test_mixed_step_graph_replay(gpu, name):
             del junk
     finally:
         L.hip_graph_destroy(g)
+
+
+@pytest.mark.parametrize("name", ["c3", "kt_prefill"])
+def test_pure_prefill_graph_replay(gpu, name):
+    """A pure prefill step at GQA 2 (the key-split kernel, no decode-row launch) captured into a graph: three
+    replays with eager torch work between them each give the eager step's output bit for bit."""
+    wl = make(name)
+    print(f"[gpu-test] pure prefill graph {name}", flush=True)
+    t = wl.tensors(device="cuda")
+    A.init_device()
+    L = lib()
+    meta = wl.meta(L.hip_attn_prefill_tile())
+    assert not meta.decode and meta.single_rows() == 0 and wl.nq // wl.nkv == 2
+    ws = A.Workspace.allocate(wl.nq, wl.hd, meta.n_seq, wl.max_model_len, meta_elems=meta.packed().size)
+    mgr = A.PagedAttentionManager()
+    mgr.layers[0] = A.LayerState(t["kc"].clone(), t["vc"].clone())
+    A.g_attn_mgr = mgr
+    A.bind_step(meta, ws, wl.nq, wl.nkv, wl.hd, wl.block_size, wl.max_blocks, wl.max_model_len)
+    node_out = torch.full((wl.n_tok, wl.nq, wl.hd), float("nan"), dtype=torch.bfloat16, device="cuda")
+    node = A.AttnNode(node_out, [t["q"], t["k"], t["v"]], layer_id=0)
+    A.PagedAttentionImpl.execute(0, node)
+    torch.cuda.synchronize()
+    check_hip_error(name)
+    ref = to_u16(node_out).copy()
+    assert L.hip_graph_begin() == 0
+    A.PagedAttentionImpl.execute(0, node)
+    g = L.hip_graph_end()
+    assert g
+    try:
+        for i in range(3):
+            node_out.fill_(float("nan"))
+            junk = torch.randn(1 << 20, device="cuda").sum()  # eager work between the replays
+            torch.cuda.synchronize()
+            L.hip_graph_launch(g)
+            torch.cuda.synchronize()
+            check_hip_error(f"{name} replay {i}")
+            np.testing.assert_array_equal(to_u16(node_out), ref)
+            del junk
+    finally:
+        L.hip_graph_destroy(g)

@@ -69,3 +69,37 @@ def test_noalloc_decode_rejects_oversized_launch(gpu):
     torch.cuda.synchronize()
     check_hip_error("noalloc oversized")
     np.testing.assert_array_equal(to_u16(out), before)
+
+
+def test_noalloc_decode_replays_from_a_graph(gpu):
+    """The allocation-free decode recorded into a graph (the use it exists for) and replayed three times with eager
+    calls of other sizes between the replays (which rewrite the shared array): every replay equals
+    hip_attn_decode with caller scratch, bit for bit."""
+    from llmgen_amd.attention import init_device
+
+    print("[gpu-test] noalloc graph", flush=True)
+    init_device()
+    L = lib()
+    wl, n, q, kc, vc, bt, ctx = _decode_inputs("c1")  # 4 partial parts per (sequence, head): the array is used
+    ref, got = _both(wl, n, q, kc, vc, bt, ctx)  # eager first call (takes the array's address outside capture)
+    np.testing.assert_array_equal(got, ref)
+    ps, mp = S.part_size(n), S.max_parts(n, wl.max_model_len)
+    out = torch.full((n, wl.nq, wl.hd), float("nan"), dtype=torch.bfloat16, device="cuda")
+    args = (out.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(), bt.data_ptr(), ctx.data_ptr(), n, wl.nq,
+            wl.nkv, wl.hd, wl.max_blocks, wl.block_size, wl.scale, ps, mp)
+    assert L.hip_graph_begin() == 0
+    L.hip_attn_decode_noalloc(*args)
+    g = L.hip_graph_end()
+    assert g
+    try:
+        other = _decode_inputs("kt_decode")
+        for i in range(3):
+            out.fill_(float("nan"))
+            torch.cuda.synchronize()
+            L.hip_graph_launch(g)
+            torch.cuda.synchronize()
+            check_hip_error(f"noalloc graph replay {i}")
+            np.testing.assert_array_equal(to_u16(out), ref)
+            _both(*other)  # eager calls of another shape between the replays
+    finally:
+        L.hip_graph_destroy(g)
