@@ -4,7 +4,8 @@ cases.  The shapes stay small enough for the CPU oracle (a few seconds per case)
 structural boundaries: spans shorter and longer than one decode round, several split-K parts, prefill tiles that
 straddle blocks, block sizes that are not powers of two, and 1-key contexts.
 
-Tolerance (all rows): max-abs <= 2e-2 and rel-L2 <= 1e-2 against the oracle's f32 output; the KV cache written by
+Tolerance (all rows): max-abs <= 2e-2 and rel-L2 <= 1e-2 against the oracle's f32 output (the wide cases scale the
+element bound with the output, see their test); the KV cache written by
 the step is compared bit for bit."""
 from __future__ import annotations
 
@@ -100,6 +101,69 @@ def test_random_step_matches_oracle(gpu, case):
     compare(to_u16(out), of, wl.name)
 
 
+WIDE_CASES = list(range(24))
+
+
+def _wide_workload(case: int) -> Workload:
+    """A wider net: block sizes down to 1 and up to 512 (odd ones take the per-lane DMA path), GQA 1-16, 1-4 KV
+    heads up to 8, contexts up to 5000, graph-bucket padding rows on decode steps, and input scales 0.5-2."""
+    rng = np.random.default_rng(5000 + case)
+    G = int(rng.choice([1, 2, 4, 8, 16]))
+    nkv = int(rng.choice([1, 2, 4, 8]))
+    bs = int(rng.choice([1, 2, 3, 5, 8, 16, 24, 32, 64, 100, 128, 256, 512]))
+    kind = int(rng.integers(0, 3))  # 0 decode-only, 1 prefill-only, 2 mixed
+    S = int(rng.integers(1, 12))
+    spec = []
+    for _ in range(S):
+        ctx = int(rng.integers(1, 5000))
+        k = kind if kind < 2 else int(rng.integers(0, 3))
+        if k == 0:
+            spec.append((ctx - 1, 1))
+        elif k == 1:
+            spec.append((0, min(ctx, int(rng.integers(2, 700)))))
+        else:
+            spec.append((ctx, int(rng.integers(2, 300))))
+    ctxs = [a + b for a, b in spec]
+    tables, nb = _tables(rng, ctxs, bs, permute=True, extra_blocks=3)
+    mb = max(len(t) for t in tables)
+    pad = int(rng.integers(0, 3)) if kind == 0 else 0
+    return Workload(f"wide{case}", G * nkv, nkv, 128, bs, nb, mb, mb * bs,
+                    [Entry(a, b, t) for (a, b), t in zip(spec, tables)], std=float(rng.choice([0.5, 1.0, 2.0])),
+                    seed=7000 + case, decode=None if kind == 0 else False, pad_rows=pad,
+                    note=f"wide: G={G} nkv={nkv} bs={bs} S={S} kind={kind} pad={pad}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", WIDE_CASES)
+def test_wide_random_step_matches_oracle(gpu, case):
+    """As above on the wider net.  At input scale 2 the outputs reach |o| of 5-8, whose own bf16 rounding is up to
+    2^-9 |o|, so the element bound is 2e-2 + 2^-6 |o| (2e-2 flat at the configs' scales); rel-L2 <= 1e-2 as
+    everywhere.  Steps of more than 400 rows are checked on 200 seeded rows."""
+    import oracle
+
+    wl = _wide_workload(case)
+    print(f"[gpu-test] {wl.name}: {wl.note} std={wl.std}", flush=True)
+    t = wl.tensors(device="cuda")
+    out, kc, vc = run_gpu(wl, t)
+    n = wl.n_tok
+    rows = None
+    if n > 400:
+        rows = np.array(sorted(set(np.random.default_rng(case).integers(0, n, size=200).tolist())), np.int32)
+    okc, ovc, _, of = run_oracle(wl, t, rows=rows, threads=16)
+    assert_cache_equal(to_u16(kc), okc, f"{wl.name} store_kv K")
+    assert_cache_equal(to_u16(vc), ovc, f"{wl.name} store_kv V")
+    got = to_u16(out) if rows is None else to_u16(out)[rows]
+    g = oracle.bf16_to_f32(got).astype(np.float64)
+    r = of.astype(np.float64)
+    assert np.isfinite(g).all(), f"{wl.name}: non-finite outputs"
+    err = np.abs(g - r)
+    bound = 2e-2 + np.abs(r) * 2.0 ** -6
+    worst = np.unravel_index(int((err - bound).argmax()), err.shape)
+    assert (err <= bound).all(), f"{wl.name}: error {err[worst]:.4g} beyond {bound[worst]:.4g} at {worst}"
+    rel = float(np.linalg.norm(g - r) / max(float(np.linalg.norm(r)), 1e-30))
+    assert rel <= 1e-2, f"{wl.name}: rel-L2 {rel:.4g}"
+
+
 def test_random_shapes_are_valid():
     """CPU check of the generator: every case builds step metadata, and the cases cover both step kinds, several
     group sizes and block sizes."""
@@ -119,3 +183,5 @@ def test_random_shapes_are_valid():
         assert meta.single_rows() == 0 and not meta.decode
         bss.add(wl.block_size)
     assert len(bss) >= 3
+    wide_bs = {_wide_workload(c).block_size for c in WIDE_CASES}
+    assert len(wide_bs) >= 6 and min(wide_bs) <= 3
