@@ -494,11 +494,14 @@ extern "C" void hip_attn_prefill_rows(bf16_t *out, const bf16_t *q, const bf16_t
         case 1: launch_prefill<2>(mode, head_groups, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq,
                                   tile_q0, n_tiles, nq, nkv, G, max_blocks, block_size, bs_shift, sl2); break;
         case 2:
-            // Pure prefill: 8-wave workgroups whose two key groups split each unit's key tiles, so the heaviest
-            // units (the long prompt's last tiles) take half as many iterations (c3 -7 %).  With decode rows beside
-            // it (single_rows != 0) a 128 KB workgroup finds no room next to the decode kernel's waves, and 4-wave
-            // workgroups (two per CU) are faster (c4 +9 % otherwise).
-            if (single_rows == 0)
+            // Pure prefill of up to 2.5 units per CU: 8-wave workgroups whose two key groups split each unit's key
+            // tiles, so the heaviest units (a long prompt's last tiles) take half as many iterations (c3 -7 %;
+            // measured on single prompts: 64 against 75 us at 3584 tokens, even at 4608).  Larger steps are
+            // bound by throughput, where the 4-wave workgroups (two per CU) are faster (5632 tokens: 137 against
+            // 148 us; 16384: 986 against 1069 us).  With decode rows beside it (single_rows != 0) a 128 KB
+            // workgroup finds no room next to the decode kernel's waves, and 4-wave workgroups are faster (c4 +9 %
+            // otherwise).
+            if (single_rows == 0 && (long)n_tiles * nkv * head_groups * 2 <= 5L * llmgen_num_cus())
                 launch_prefill<8, 2>(mode, head_groups, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q,
                                      tile_seq, tile_q0, n_tiles, nq, nkv, G, max_blocks, block_size, bs_shift, sl2);
             else
