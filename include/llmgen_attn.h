@@ -90,8 +90,9 @@ void hip_attn_prefill(uint16_t *out, const uint16_t *q, const uint16_t *k_cache,
  * as one-row prefill tiles); the executor slice (llmgen_paged_attention) passes the count it has from its
  * entries, so a pure prefill step does not pay for a grid of workgroups that find nothing to do.  The count must be
  * exact when it is 0: a step that has single-row segments but is passed 0 leaves those rows unwritten (pass -1
- * when unsure).  For GQA 2 a count of 0 also selects the key-split prefill kernel, whose outputs differ from
- * hip_attn_prefill's in the last bits (another summation order, same tolerance). */
+ * when unsure).  For GQA >= 2 a count of 0 also selects, on steps of at most 2.5 (query tile, KV head, head pair)
+ * units per CU, the key-split prefill kernel, whose outputs differ from hip_attn_prefill's in the last bits (another
+ * summation order, same tolerance). */
 void hip_attn_prefill_rows(uint16_t *out, const uint16_t *q, const uint16_t *k_cache, const uint16_t *v_cache,
                            const int32_t *block_tables, const int32_t *ctx_lens, const int32_t *cu_q,
                            const int32_t *tile_seq, const int32_t *tile_q0, int n_tiles, int nq, int nkv, int hd,

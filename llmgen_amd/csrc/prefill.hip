@@ -478,7 +478,11 @@ extern "C" void hip_attn_prefill_rows(bf16_t *out, const bf16_t *q, const bf16_t
     const int mode = (bs_shift >= 0 && block_size % BK == 0) ? DMA_BLOCK : (block_size % 4 == 0 ? DMA_ROW4 : DMA_FLAT);
     const float sl2 = scale * LLMGEN_LOG2E;
     // two waves per head; at most 8 waves (4 heads) per workgroup, the rest of the group in further workgroups
-    const int heads_per_wg = G < 4 ? G : 4;
+    int heads_per_wg = G < 4 ? G : 4;
+    // A small pure-prefill step at G >= 4 runs as G / 2 two-head groups so that it can take the key-split
+    // workgroups below (single G = 4 prompt of 2048 tokens: 47 against 57 us; at 3584 tokens, 896 units, the
+    // 8-wave four-head workgroups stay faster: 105 against 112-122 us)
+    if (single_rows == 0 && G >= 4 && (long)n_tiles * nkv * (G / 2) * 2 <= 5L * llmgen_num_cus()) heads_per_wg = 2;
     const int head_groups = G / heads_per_wg;
     // Decode rows (q_len == 1) go to the bandwidth-oriented decode kernel on the side stream, concurrently with
     // the MFMA kernel (which skips them) on the launch stream: HBM-bound and MFMA-bound work overlap.  Its grid
