@@ -85,25 +85,26 @@ class Step:
     def __init__(self, name: str):
         import torch
         from llmgen_amd import attention as A
+        from llmgen_amd import host as H
         from llmgen_amd._lib import lib
         from llmgen_amd.workloads import make
 
         self.L = lib()
         self.wl = wl = make(name)
         self.t = wl.tensors(device="cuda")
-        self.meta = wl.meta(self.L.hip_attn_prefill_tile())
-        self.ws = A.Workspace.allocate(wl.nq, wl.hd, self.meta.n_seq, wl.max_model_len,
-                                       meta_elems=self.meta.packed().size)
+        self.meta = wl.meta(self.L.hip_attn_prefill_tile())  # the Python restatement: the CPU baseline's input
+        self.ws = wl.workspace()
         self.layer = A.LayerState(self.t["kc"].clone(), self.t["vc"].clone())
         mgr = A.PagedAttentionManager()
         mgr.layers[0] = self.layer
         A.g_attn_mgr = mgr
-        # a private copy: later bind_step calls (graph capture) rewrite the global g_step
-        self.g = copy.copy(A.bind_step(self.meta, self.ws, wl.nq, wl.nkv, wl.hd, wl.block_size, wl.max_blocks,
-                                       wl.max_model_len))
+        # the StepState the C++ executor slice binds (fillMeta + bindStep); a private copy, since later binds
+        # rewrite the global g_step
+        self.g = H.StepState.from_buffer_copy(wl.bind(self.ws))
         self.out = torch.zeros(wl.n_tok, wl.nq, wl.hd, dtype=torch.bfloat16, device="cuda")
         self.node = A.AttnNode(self.out, [self.t["q"], self.t["k"], self.t["v"]], layer_id=0)
         self.A = A
+        self.H = H
         # write this step's K/V once so attention-only launches see the full context
         self.store_kv()
         pool_bytes = 2 * self.layer.k.numel() * self.layer.k.element_size()
@@ -119,23 +120,13 @@ class Step:
                             self.layer.v.data_ptr(), g.n_tok, wl.nkv, wl.hd, wl.block_size)
 
     def attn(self):
-        """The attention launcher alone (decode or prefill), as PagedAttentionImpl issues it after store_kv.
-        Successive calls read successive copies of the KV pools (cold in every cache)."""
-        from llmgen_amd import step as S
-
-        g, wl = self.g, self.wl
+        """The attention launch alone, exactly as the engine's operator issues it after store_kv: the C++
+        llmgen_paged_attention with the StepState the C++ bind produced (hip_attn_decode for a decode step,
+        hip_attn_prefill_rows with the step's single-row count otherwise).  Successive calls read successive
+        copies of the KV pools (cold in every cache)."""
         kc, vc = self.pools[self._turn % len(self.pools)]
         self._turn += 1
-        if g.decode:
-            self.L.hip_attn_decode(self.out.data_ptr(), self.t["q"].data_ptr(), kc.data_ptr(), vc.data_ptr(),
-                                   g.block_tables, g.ctx, g.n_seq, wl.nq, wl.nkv, wl.hd,
-                                   wl.max_blocks, wl.block_size, g.attn_scale, g.part_o, g.part_ml,
-                                   S.part_size(g.n_seq), S.max_parts(g.n_seq, wl.max_model_len))
-        else:
-            self.L.hip_attn_prefill_rows(self.out.data_ptr(), self.t["q"].data_ptr(), kc.data_ptr(),
-                                         vc.data_ptr(), g.block_tables, g.ctx, g.cu_q, g.tile_seq,
-                                         g.tile_q0, g.n_tiles, wl.nq, wl.nkv, wl.hd, wl.max_blocks, wl.block_size,
-                                         g.attn_scale, g.single_rows)
+        self.H.paged_attention(self.g, self.out, self.t["q"], None, None, kc, vc, store_kv=False)
 
     def full_step(self):
         self.A.PagedAttentionImpl.execute(0, self.node)

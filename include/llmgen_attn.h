@@ -44,7 +44,10 @@ void hip_store_kv(const uint16_t *k, const uint16_t *v, const int32_t *slot_mapp
  * Split-K scratch is owned by the caller: part_o [S, nq, max_parts, hd] f32 and part_ml [S, nq, max_parts, 2]
  * f32 (attention_v1.zig:51-57 partSize / maxParts; executor.zig:92-102 sizing).  Part p covers tokens
  * [p * part_size, (p + 1) * part_size); tokens past max_parts * part_size are not attended (as in the
- * reference).  ctx <= 0 rows output 0.  Requires hd == 128 and nq / nkv in {1, 2, 4, 8, 16}. */
+ * reference).  ctx <= 0 rows output 0.  Requires hd == 128 and nq / nkv in {1, 2, 4, 8, 16}.
+ * Split launches merge their partials in the kernel, elected by per-(sequence, kv head) counters in a library-owned
+ * device array that return to 0 after every launch: launches of the decode entry points that overlap on one
+ * device (two streams) race on them and must be serialised by the caller. */
 void hip_attn_decode(uint16_t *out, const uint16_t *q, const uint16_t *k_cache, const uint16_t *v_cache,
                      const int32_t *block_tables, const int32_t *ctx_lens, int S, int nq, int nkv, int hd,
                      int max_blocks, int block_size, float scale, float *part_o, float *part_ml, int part_size,
@@ -65,10 +68,14 @@ void hip_attn_decode_store_kv(uint16_t *out, const uint16_t *q, const uint16_t *
  * graph capture, tight serving loops, harnesses that forbid hipMalloc): the split-K partials live in the
  * library's own file-scope device array of 8 MiB per device instead of caller-owned part_o / part_ml, so the
  * call allocates nothing.  Arguments and output as hip_attn_decode (part_size / max_parts as the engine computes
- * them).  A launch whose partials need more than 8 MiB (S * nq * parts-per-sequence * 520 bytes, where the
- * launcher keeps parts-per-sequence small: about 512 / (S * nkv) for long contexts, at least 1) prints one line
- * and launches nothing.  All calls on one device share the array: calls that overlap on one device (two streams)
- * race and must be serialised by the caller. */
+ * them).  A launch with one part per (sequence, head) stores no partials and needs none of the array, whatever
+ * its size.  A launch whose partials need more than 8 MiB (S * nq * parts-per-sequence * 520 bytes; the launcher
+ * keeps parts-per-sequence near 512 / (S * nkv) or below, so in practice only single-sequence launches with over
+ * 1000 parts at GQA 16 reach it) prints one line, launches nothing and records hipErrorInvalidValue, which the next
+ * hip_last_error() returns.  All calls on one device share the array and also the per-(sequence, kv head) merge
+ * counters that hip_attn_decode and hip_attn_decode_store_kv use: calls of any of the three that overlap on one
+ * device (two streams) race on the counters and, for this entry point, on the array, and must be serialised by
+ * the caller. */
 void hip_attn_decode_noalloc(uint16_t *out, const uint16_t *q, const uint16_t *k_cache, const uint16_t *v_cache,
                              const int32_t *block_tables, const int32_t *ctx_lens, int S, int nq, int nkv, int hd,
                              int max_blocks, int block_size, float scale, int part_size, int max_parts);
@@ -128,7 +135,8 @@ int hip_attn_set_option(int option, int value);
 int hip_init(size_t ws_bytes);
 /* Replaces cuda_sync: waits for the stream. */
 void hip_sync(void);
-/* Replaces cuda_last_error: hipGetLastError(), 0 = no error. */
+/* Replaces cuda_last_error: 0 = no error.  Returns an error the library recorded when it rejected a launch on the
+ * host (hip_attn_decode_noalloc), else hipGetLastError(); either is cleared by the read. */
 int hip_last_error(void);
 /* Replace cuda_graph_begin / _end / _launch / _destroy: capture on the stream (thread-local mode),
  * end + instantiate (returns a hipGraphExec_t or NULL), replay, destroy. */

@@ -59,8 +59,8 @@ typedef struct llmgen_step_state {
     void *seed, *pos, *slots, *cu_q, *ctx, *last, *temps, *tile_seq, *tile_q0, *block_tables;
     void *cos_sin, *part_o, *part_ml, *sample_scratch;
     int32_t single_rows; /* segments with one query row (decode / padding rows); -1 = unknown.  Not in the
-                            reference's StepState: bind_step sets -1, the caller sets the count it knows
-                            (llmgen_single_rows) and llmgen_paged_attention passes it to hip_attn_prefill_rows. */
+                            reference's StepState: llmgen_fill_meta returns the count and llmgen_bind_step stores
+                            it; llmgen_paged_attention passes it to hip_attn_prefill_rows. */
 } llmgen_step_state;
 
 llmgen_layout llmgen_layout_init(size_t n_tok, size_t n_seq, size_t n_tiles, size_t max_blocks);
@@ -75,18 +75,24 @@ int llmgen_step_tiles(const llmgen_entry *entries, int n_entries, int pf_tile);
 int llmgen_single_rows(const llmgen_entry *entries, int n_entries, int seq_num);
 
 /* executor.zig:772-861.  Writes the step into meta_host (lay.total bytes).  seq_num >= n_entries adds padding
- * rows (id 0, pos 0, slot -1, ctx 0, temperature 0, zero block-table row).  *step_seed advances by the
- * golden-ratio increment and is stored in the seed segment.  slot = block_table[p / bs] * bs + p % bs
- * (batching.zig:74-77). */
+ * rows (id 0, pos 0, slot -1, ctx 0, temperature 0, zero block-table row); in a step with prefill tiles
+ * (n_tiles > 0) each padding row also gets a tile of its own, so n_tiles must count them.  *step_seed advances by
+ * the golden-ratio increment and is stored in the seed segment.  slot = block_table[p / bs] * bs + p % bs
+ * (batching.zig:74-77).  Prefill tiles are listed lightest first (by the keys a tile needs, stable), the reverse
+ * of the prefill kernel's dispatch order, so that the heaviest tiles start first; the reference lists them in
+ * entry order.  Returns the step's count of single-row segments (>= 0, llmgen_single_rows), which
+ * llmgen_bind_step takes, or a negative value if the step does not fit the layout or is malformed. */
 int llmgen_fill_meta(uint8_t *meta_host, llmgen_layout lay, const llmgen_seq *seqs, const llmgen_entry *entries,
                      int n_entries, int seq_num, int n_tiles, int pf_tile, int block_size, int max_blocks,
                      uint64_t *step_seed);
 
 /* executor.zig:864-895: fill st with the step's sizes, the model's head shape and the device addresses of the
- * metadata segments in meta_dev (attn_scale = 1 / sqrtf(head_dim)). */
+ * metadata segments in meta_dev (attn_scale = 1 / sqrtf(head_dim)).  single_rows is llmgen_fill_meta's return
+ * value for this step (-1 if unknown: the prefill launcher then always runs its single-row launch and never the
+ * key-split kernel). */
 void llmgen_bind_step(llmgen_step_state *st, void *meta_dev, llmgen_layout lay, int n_tok, int n_seq, int n_tiles,
                       int decode, int hidden, int n_head, int n_kv_head, int head_dim, int block_size, int max_blocks,
-                      size_t max_model_len, void *part_o, void *part_ml, void *sample_scratch);
+                      size_t max_model_len, void *part_o, void *part_ml, void *sample_scratch, int single_rows);
 
 /* attention_v1.zig:60-120 PagedAttentionImpl.execute for one layer: store_kv of the step's k / v (unless
  * store_kv == 0: already written, e.g. by hip_qk_norm_rope_store_kv), then split-K decode or causal prefill.

@@ -3,12 +3,16 @@
 The reference engine dispatches the ``OP_TYPE_PAGED_ATTN`` node to ``PagedAttentionImpl(device).execute(device_id,
 out)`` (``src/ops.zig:63-65, 197-209``), which reads every per-step value from the global ``g_step``
 (``src/backend/cpu/common.zig:10-43``) and the layer's KV pools from ``kvOf(layer_id)`` (``common.zig:46-52``).
-This module keeps those names, argument meanings and error behaviour, and drives ``libllmgen_attn.so``:
+This module keeps those names, argument meanings and error behaviour.  It holds no host logic of its own: the
+step metadata, the StepState and the per-layer dispatch are the C++ executor slice in ``libllmgen_attn.so``
+(``include/llmgen_host.h``), reached through :mod:`llmgen_amd.host`:
 
-* :class:`StepState` / :data:`g_step` -- the attention fields of ``common.StepState`` (device pointers as ints).
+* :data:`g_step` -- the C++ ``llmgen_step_state`` (``common.StepState``) of the bound step.
 * :class:`PagedAttentionManager` / :func:`kv_of` -- per-layer K/V pools (``memory/page_atten.zig:15-28``).
-* :class:`PagedAttentionImpl` -- ``attention_v1.zig:60-120``: store_kv, then decode (split-K) or prefill.
-* :func:`bind_step` -- ``executor.zig:864-895`` bindStep: uploads the packed metadata and fills ``g_step``.
+* :class:`PagedAttentionImpl` -- ``attention_v1.zig:60-120``: checks as the Zig operator does, then
+  ``llmgen_paged_attention`` (store_kv, then decode or prefill).
+* :func:`bind_step` -- ``executor.zig:772-895`` fillMeta + bindStep: ``llmgen_fill_meta`` packs the step, one
+  host-to-device copy uploads it, ``llmgen_bind_step`` fills ``g_step``.
 
 Tensors are torch tensors on the GPU (torch is used for device memory only); bf16 tensors may be
 ``torch.bfloat16`` or ``torch.int16``/``uint16`` views of the same bits.
@@ -22,6 +26,7 @@ from typing import Dict, List, Optional
 import numpy as np
 import torch
 
+from . import host as H
 from . import step as stepmod
 from ._lib import lib
 
@@ -38,35 +43,7 @@ class LayerNotActive(KeyError):
     """common.zig:51 error.LayerNotActive."""
 
 
-@dataclass
-class StepState:
-    """common.zig:10-41 (the fields attention reads). Pointers are device addresses (int)."""
-
-    n_tok: int = 0
-    n_seq: int = 0
-    n_tiles: int = 0
-    decode: bool = False
-    n_head: int = 0
-    n_kv_head: int = 0
-    head_dim: int = 0
-    attn_scale: float = 0.0
-    block_size: int = 0
-    max_blocks: int = 0
-    max_model_len: int = 0
-    pos: int = 0
-    slots: int = 0
-    cu_q: int = 0
-    ctx: int = 0
-    last: int = 0
-    tile_seq: int = 0
-    tile_q0: int = 0
-    block_tables: int = 0
-    part_o: int = 0
-    part_ml: int = 0
-    single_rows: int = -1  # segments with one query row (-1 unknown); not in the reference's StepState
-
-
-g_step = StepState()
+g_step = H.StepState()  # the bound step (C++ llmgen_step_state)
 
 
 @dataclass
@@ -126,8 +103,10 @@ def _ptr(t: torch.Tensor) -> int:
 
 
 class PagedAttentionImpl:
-    """attention_v1.zig:60-120 for the HIP backend.  Decode steps issue store_kv and split-K decode as one fused
-    launch (hip_attn_decode_store_kv); prefill / mixed steps issue store_kv, then prefill, as the reference does."""
+    """attention_v1.zig:60-120 for the HIP backend: the checks of the Zig operator, then the C++
+    ``llmgen_paged_attention``.  Decode steps issue store_kv and split-K decode as one fused launch
+    (hip_attn_decode_store_kv); prefill / mixed steps issue store_kv, then prefill with the step's single-row
+    count, as the reference issues store_kv then prefill."""
 
     @staticmethod
     def execute(device_id: int, out: AttnNode, store_kv: bool = True) -> None:
@@ -135,29 +114,12 @@ class PagedAttentionImpl:
         hip_qk_norm_rope_store_kv); ``out.src[1:]`` are then not read."""
         if out.data.dtype not in _BF16_LIKE:
             raise AttentionNeedsBf16(f"attention needs bf16, got {out.data.dtype}")
-        s = g_step
         kv = kv_of(out.layer_id)
-        L = lib()
         q, k, v = out.src
-        if s.decode and store_kv:
-            # store_kv fused into the decode launch (one kernel per decode step)
-            L.hip_attn_decode_store_kv(_ptr(out.data), _ptr(q), _ptr(k), _ptr(v), s.slots, _ptr(kv.k), _ptr(kv.v),
-                                       s.block_tables, s.ctx, s.n_seq, s.n_head, s.n_kv_head, s.head_dim,
-                                       s.max_blocks, s.block_size, s.attn_scale, s.part_o, s.part_ml,
-                                       stepmod.part_size(s.n_seq), stepmod.max_parts(s.n_seq, s.max_model_len))
-            return
-        if store_kv:
-            L.hip_store_kv(_ptr(k), _ptr(v), s.slots, _ptr(kv.k), _ptr(kv.v), s.n_tok, s.n_kv_head, s.head_dim,
-                           s.block_size)
-        if s.decode:
-            L.hip_attn_decode(_ptr(out.data), _ptr(q), _ptr(kv.k), _ptr(kv.v), s.block_tables, s.ctx, s.n_seq,
-                              s.n_head, s.n_kv_head, s.head_dim, s.max_blocks, s.block_size, s.attn_scale,
-                              s.part_o, s.part_ml, stepmod.part_size(s.n_seq),
-                              stepmod.max_parts(s.n_seq, s.max_model_len))
-        else:
-            L.hip_attn_prefill_rows(_ptr(out.data), _ptr(q), _ptr(kv.k), _ptr(kv.v), s.block_tables, s.ctx,
-                                    s.cu_q, s.tile_seq, s.tile_q0, s.n_tiles, s.n_head, s.n_kv_head, s.head_dim,
-                                    s.max_blocks, s.block_size, s.attn_scale, s.single_rows)
+        for t in (out.data, q, kv.k, kv.v) + ((k, v) if store_kv else ()):
+            _ptr(t)
+        H.paged_attention(g_step, out.data, q, k if store_kv else None, v if store_kv else None, kv.k, kv.v,
+                          store_kv=store_kv)
 
 
 # attention_v1.zig:123: the legacy FLASH_ATTN node runs the same implementation
@@ -169,40 +131,63 @@ class Workspace:
     """Device buffers the executor owns for attention: packed step metadata and split-K scratch
     (executor.zig:81-112)."""
 
-    meta: torch.Tensor
+    meta: torch.Tensor  # uint8, at least the packed layout's bytes
     part_o: torch.Tensor
     part_ml: torch.Tensor
 
     @staticmethod
-    def allocate(nq: int, hd: int, max_seqs: int, max_model_len: int, meta_elems: int,
+    def allocate(nq: int, hd: int, max_seqs: int, max_model_len: int, meta_bytes: int,
                  device="cuda") -> "Workspace":
         po, pml = stepmod.workspace_bytes(nq, hd, max_seqs, max_model_len)
-        return Workspace(meta=torch.zeros(meta_elems, dtype=torch.int32, device=device),
+        return Workspace(meta=torch.zeros(meta_bytes, dtype=torch.uint8, device=device),
                          part_o=torch.empty(po // 4, dtype=torch.float32, device=device),
                          part_ml=torch.empty(pml // 4, dtype=torch.float32, device=device))
 
 
-def bind_step(meta: "stepmod.StepMeta", ws: Workspace, nq: int, nkv: int, hd: int, block_size: int,
-              max_blocks: int, max_model_len: int, upload: bool = True) -> StepState:
-    """executor.zig:864-895: upload the packed metadata (one host-to-device copy) and publish its device
-    addresses in g_step."""
-    buf = meta.packed()
+def _step_shape(entries, seq_num, decode, pf_tile):
+    n_pad = seq_num - len(entries)
+    if n_pad < 0:
+        raise ValueError("seq_num < number of entries")
+    if decode is None:  # the engine's rule (executor.zig:530-552)
+        decode = all(e.q_len == 1 and e.emits for e in entries)
+    n_tok = sum(e.q_len for e in entries) + n_pad
+    n_tiles = 0 if decode else sum((e.q_len + pf_tile - 1) // pf_tile for e in entries) + n_pad
+    return bool(decode), n_tok, n_tiles
+
+
+def meta_bytes(entries, max_blocks: int, seq_num: Optional[int] = None, decode: Optional[bool] = None) -> int:
+    """Bytes of the packed metadata of this step (the C++ layout, executor.zig:139-202)."""
+    seq_num = len(entries) if seq_num is None else seq_num
+    _, n_tok, n_tiles = _step_shape(entries, seq_num, decode, lib().hip_attn_prefill_tile())
+    return H.layout(n_tok, seq_num, n_tiles, max_blocks).total
+
+
+def bind_step(entries, ws: Workspace, nq: int, nkv: int, hd: int, block_size: int, max_blocks: int,
+              max_model_len: int, seq_num: Optional[int] = None, decode: Optional[bool] = None,
+              upload: bool = True) -> "H.StepState":
+    """executor.zig:772-895 for one step: ``llmgen_fill_meta`` packs the step (slots, cu_q, ctx, prefill tiles
+    lightest first, block tables, padding rows up to ``seq_num``), one host-to-device copy uploads it, and
+    ``llmgen_bind_step`` publishes its device addresses and the single-row count in :data:`g_step`.
+
+    ``entries``: :class:`~llmgen_amd.step.Entry` (q_start, q_len, block_table, emits).  ``decode`` defaults to
+    the engine's rule (every entry has q_len == 1 and emits).  Attention reads no token ids, so the sequences
+    handed to fillMeta carry zeros."""
+    global g_step
+    seq_num = len(entries) if seq_num is None else seq_num
+    pf = lib().hip_attn_prefill_tile()
+    decode, n_tok, n_tiles = _step_shape(entries, seq_num, decode, pf)
+    seqs = [H.Sequence_([0] * (e.q_start + e.q_len + (0 if e.emits else 1)), list(e.block_table))
+            for e in entries]
+    ents = [(i, e.q_start, e.q_len) for i, e in enumerate(entries)]
+    buf, lay, _, single = H.fill_meta(seqs, ents, seq_num, n_tiles, pf, block_size, max_blocks)
     if buf.size > ws.meta.numel():
         raise ValueError("step metadata does not fit the workspace")
     if upload:
         ws.meta[:buf.size].copy_(torch.from_numpy(buf), non_blocking=False)
-    base = ws.meta.data_ptr()
-    off = meta.offsets
-    g = g_step
-    g.n_tok, g.n_seq, g.n_tiles, g.decode = meta.n_tok, meta.n_seq, meta.n_tiles, meta.decode
-    g.n_head, g.n_kv_head, g.head_dim = nq, nkv, hd
-    g.attn_scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))  # f32, as executor.zig:877
-    g.block_size, g.max_blocks, g.max_model_len = block_size, max_blocks, max_model_len
-    for name in ("pos", "slots", "cu_q", "ctx", "last", "tile_seq", "tile_q0", "block_tables"):
-        setattr(g, name, base + 4 * off[name])
-    g.part_o, g.part_ml = ws.part_o.data_ptr(), ws.part_ml.data_ptr()
-    g.single_rows = meta.single_rows()
-    return g
+    g_step = H.bind_step(ws.meta.data_ptr(), lay, n_tok, seq_num, n_tiles, decode, nq, nkv, hd, block_size,
+                         max_blocks, max_model_len, ws.part_o.data_ptr(), ws.part_ml.data_ptr(),
+                         single_rows=single)
+    return g_step
 
 
 _inited = False

@@ -659,17 +659,26 @@ void decode_launch(bf16_t *out, const bf16_t *q, const bf16_t *k_new, const bf16
     const int nparts = (max_parts + k - 1) / k;
     const int span = (int)std::min((long)part_size * k, 1L << 30);  // tokens per workgroup (no int overflow)
     int stride = max_parts;  // partial slots per (sequence, head) in part_o / part_ml
-    if (own_scratch) {
+    // With one part per (sequence, head) every workgroup writes its rows directly and no partial is stored or
+    // read (the merge kernel returns early), so the library's array is not needed.
+    if (own_scratch && nparts == 1) {
+        part_o = part_ml = nullptr;
+        stride = 1;
+    } else if (own_scratch) {
         const size_t rows = (size_t)S * nq * nparts;
         if (rows * (HD + 2) > NOALLOC_SCRATCH_FLOATS) {
             fprintf(stderr,
                     "[llmgen-hip] attn_decode_noalloc: this launch needs %zu bytes of split-K scratch, more than the "
                     "library's %zu; use hip_attn_decode with caller-owned scratch\n",
                     rows * (HD + 2) * sizeof(float), NOALLOC_SCRATCH_FLOATS * sizeof(float));
+            llmgen_record_error(hipErrorInvalidValue);
             return;
         }
         float *base = noalloc_scratch();
-        if (!base) return;
+        if (!base) {
+            llmgen_record_error(hipErrorInvalidSymbol);
+            return;
+        }
         part_o = base;
         part_ml = base + rows * HD;
         stride = nparts;

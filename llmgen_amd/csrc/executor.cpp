@@ -124,6 +124,26 @@ int llmgen_fill_meta(uint8_t *meta_host, llmgen_layout lay, const llmgen_seq *se
             }
         }
     }
+    // graph-bucket padding rows: ctx 0 (attention writes zeros), slot -1 (no KV write).  In a step with prefill
+    // tiles each padding row also gets a tile, so that the kernels write its zero row.
+    for (int s = n_entries; s < seq_num; ++s) {
+        if (t >= n_tok_cap) return -4;
+        ids[t] = 0;
+        pos[t] = 0;
+        slots[t] = -1;
+        ++t;
+        cu_q[s + 1] = (int32_t)t;
+        ctx[s] = 0;
+        last[s] = (int32_t)t - 1;
+        temps[s] = 0.f;
+        memset(bt + (size_t)s * max_blocks, 0, sizeof(int32_t) * max_blocks);
+        if (n_tiles > 0) {
+            if (tile >= n_tiles) return -6;
+            tseq[tile] = s;
+            tq0[tile] = 0;
+            ++tile;
+        }
+    }
     // Tiles lightest first, by the keys a tile needs (stable: entry order among equals).  The reference lists them
     // in entry order; the prefill kernel accepts any order and dispatches the list from its end, so this makes
     // its dispatch heaviest first across sequences (a long prompt's last tiles start before short prompts).
@@ -141,25 +161,12 @@ int llmgen_fill_meta(uint8_t *meta_host, llmgen_layout lay, const llmgen_seq *se
             tq0[i] = q00[order[i]];
         }
     }
-    // graph-bucket padding rows: ctx 0 (attention writes zeros), slot -1 (no KV write)
-    for (int s = n_entries; s < seq_num; ++s) {
-        if (t >= n_tok_cap) return -4;
-        ids[t] = 0;
-        pos[t] = 0;
-        slots[t] = -1;
-        ++t;
-        cu_q[s + 1] = (int32_t)t;
-        ctx[s] = 0;
-        last[s] = (int32_t)t - 1;
-        temps[s] = 0.f;
-        memset(bt + (size_t)s * max_blocks, 0, sizeof(int32_t) * max_blocks);
-    }
-    return 0;
+    return llmgen_single_rows(entries, n_entries, seq_num);
 }
 
 void llmgen_bind_step(llmgen_step_state *st, void *meta_dev, llmgen_layout lay, int n_tok, int n_seq, int n_tiles,
                       int decode, int hidden, int n_head, int n_kv_head, int head_dim, int block_size, int max_blocks,
-                      size_t max_model_len, void *part_o, void *part_ml, void *sample_scratch) {
+                      size_t max_model_len, void *part_o, void *part_ml, void *sample_scratch, int single_rows) {
     uint8_t *m = static_cast<uint8_t *>(meta_dev);
     st->n_tok = n_tok;
     st->n_seq = n_seq;
@@ -187,7 +194,7 @@ void llmgen_bind_step(llmgen_step_state *st, void *meta_dev, llmgen_layout lay, 
     st->part_o = part_o;
     st->part_ml = part_ml;
     st->sample_scratch = sample_scratch;
-    st->single_rows = -1;
+    st->single_rows = single_rows;
 }
 
 int llmgen_part_size(int n_seq) {
@@ -316,7 +323,7 @@ bool ok(hipError_t e, const char *what) {
 void run_nodes(Graphs &g, Bucket &b, int n_seq) {
     llmgen_step_state st{};
     llmgen_bind_step(&st, b.meta_dev, b.lay, n_seq, n_seq, 0, 1, 0, g.nq, g.nkv, g.hd, g.block_size, g.max_blocks,
-                     g.max_model_len, b.part_o, b.part_ml, nullptr);
+                     g.max_model_len, b.part_o, b.part_ml, nullptr, n_seq);
     for (int l = 0; l < g.n_layers; ++l) llmgen_paged_attention(&st, b.out, b.q, b.k, b.v, g.kc[l], g.vc[l], 1);
 }
 
@@ -440,7 +447,7 @@ int llmgen_graphs_step(void *graphs, const llmgen_seq *seqs, const llmgen_entry 
     // the previous step's upload must have left the pinned buffer before it is rewritten
     if (!ok(hipStreamSynchronize(stream), "sync")) return -3;
     if (llmgen_fill_meta(g->meta_host, b.lay, seqs, entries, n_entries, b.size, 0, 64, g->block_size, g->max_blocks,
-                         &g->step_seed) != 0)
+                         &g->step_seed) < 0)
         return -4;
     const size_t qrow = (size_t)g->nq * g->hd * 2, krow = (size_t)g->nkv * g->hd * 2;
     bool good = ok(hipMemcpyAsync(b.meta_dev, g->meta_host, b.lay.total, hipMemcpyHostToDevice, stream), "h2d") &&

@@ -98,3 +98,7 @@ __attribute__((visibility("hidden"))) int llmgen_opt(int which);
 
 // Internal: compute units of the current device (256 if the query fails); cached after the first call.
 __attribute__((visibility("hidden"))) int llmgen_num_cus();
+
+// Internal: record an error of the library's own (a launch rejected on the host) for hip_last_error to return;
+// the first recorded error is kept until hip_last_error reads it.
+__attribute__((visibility("hidden"))) void llmgen_record_error(hipError_t e);

@@ -10,11 +10,19 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <atomic>
+
 hipStream_t g_llmgen_stream = nullptr;
 static bool g_own_stream = false;
 static hipStream_t g_side_stream = nullptr;
 static hipEvent_t g_fork_event = nullptr, g_join_event = nullptr;
 static hipGraph_t g_capture_graph = nullptr;
+static std::atomic<int> g_own_error{0};
+
+void llmgen_record_error(hipError_t e) {
+    int zero = 0;
+    g_own_error.compare_exchange_strong(zero, (int)e);
+}
 
 #define HIP_WARN(call)                                                                                   \
     do {                                                                                                 \
@@ -197,8 +205,14 @@ void hip_d2h_async(void *dst, const void *src, size_t n) {
     HIP_WARN(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, g_llmgen_stream));
 }
 
-// cuda_context.cu:96-102.  Launches are asynchronous: errors show up after a sync.
-int hip_last_error(void) { return (int)hipGetLastError(); }
+// cuda_context.cu:96-102.  Launches are asynchronous: errors show up after a sync.  An error the library recorded
+// itself (a launch it rejected on the host, llmgen_record_error) is returned first, and cleared by the read;
+// otherwise the runtime's last error.
+int hip_last_error(void) {
+    const int own = g_own_error.exchange(0);
+    const int rt = (int)hipGetLastError();
+    return own ? own : rt;
+}
 void hip_sync(void) { HIP_WARN(hipStreamSynchronize(g_llmgen_stream)); }
 
 // cuda_context.cu:106-126.  Graph capture on the global stream.

@@ -64,7 +64,7 @@ HOST_SIGNATURES = {
                                         ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                         ctypes.POINTER(ctypes.c_uint64)]),
     "llmgen_bind_step": (None, [ctypes.POINTER(StepState), _P, Layout] + [ctypes.c_int] * 10
-                         + [_sz, _P, _P, _P]),
+                         + [_sz, _P, _P, _P, ctypes.c_int]),
     "llmgen_paged_attention": (ctypes.c_int, [ctypes.POINTER(StepState), _P, _P, _P, _P, _P, _P, ctypes.c_int]),
     "llmgen_part_size": (ctypes.c_int, [ctypes.c_int]),
     "llmgen_max_parts": (ctypes.c_int, [ctypes.c_int, _sz]),
@@ -133,7 +133,7 @@ def layout(n_tok: int, n_seq: int, n_tiles: int, max_blocks: int) -> Layout:
 
 def fill_meta(seqs: Sequence[Sequence_], entries, seq_num: int, n_tiles: int, pf_tile: int, block_size: int,
               max_blocks: int, step_seed: int = 0):
-    """Returns (packed bytes as a uint8 array, layout, new step seed)."""
+    """Returns (packed bytes as a uint8 array, layout, new step seed, the step's single-row count)."""
     n_tok = sum(e[2] for e in entries) + (seq_num - len(entries))  # padding rows carry one token each
     lay = layout(n_tok, seq_num, n_tiles, max_blocks)
     buf = np.zeros(lay.total, np.uint8)
@@ -141,9 +141,9 @@ def fill_meta(seqs: Sequence[Sequence_], entries, seq_num: int, n_tiles: int, pf
     seed = ctypes.c_uint64(step_seed)
     rc = L().llmgen_fill_meta(buf.ctypes.data, lay, sa.arr, _entries(entries), len(entries), seq_num, n_tiles,
                               pf_tile, block_size, max_blocks, ctypes.byref(seed))
-    if rc != 0:
+    if rc < 0:
         raise ValueError(f"llmgen_fill_meta rejected the step (rc={rc})")
-    return buf, lay, seed.value
+    return buf, lay, seed.value, rc
 
 
 def single_rows(entries, seq_num: int) -> int:
@@ -186,10 +186,12 @@ def workspace(n_head, head_dim, max_seqs, max_tokens, max_model_len, block_size,
 
 def bind_step(meta_dev_ptr: int, lay: Layout, n_tok, n_seq, n_tiles, decode, n_head, n_kv_head, head_dim,
               block_size, max_blocks, max_model_len, part_o=0, part_ml=0, sample_scratch=0,
-              hidden: int = 0) -> StepState:
+              hidden: int = 0, single_rows: int = -1) -> StepState:
+    """``single_rows``: llmgen_fill_meta's return value for this step (-1 if unknown)."""
     st = StepState()
     L().llmgen_bind_step(ctypes.byref(st), meta_dev_ptr, lay, n_tok, n_seq, n_tiles, int(decode), hidden, n_head,
-                         n_kv_head, head_dim, block_size, max_blocks, max_model_len, part_o, part_ml, sample_scratch)
+                         n_kv_head, head_dim, block_size, max_blocks, max_model_len, part_o, part_ml, sample_scratch,
+                         single_rows)
     return st
 
 

@@ -203,13 +203,13 @@ class Qwen3:
         n_tiles = 0 if decode else sum((e.q_len + self.pf_tile - 1) // self.pf_tile for e in entries)
         if seed is not None:
             self.step_seed = int(seed)
-        buf, lay, self.step_seed = Hx.fill_meta(seqs, ents, S, n_tiles, self.pf_tile, cfg.block_size,
-                                                self.max_blocks, self.step_seed)
+        buf, lay, self.step_seed, single = Hx.fill_meta(seqs, ents, S, n_tiles, self.pf_tile, cfg.block_size,
+                                                        self.max_blocks, self.step_seed)
         self.meta_dev[:lay.total].copy_(torch.from_numpy(buf))  # one upload per step
         g = Hx.bind_step(self.meta_dev.data_ptr(), lay, T, S, n_tiles, decode, cfg.n_head, cfg.n_kv_head,
                          cfg.head_dim, cfg.block_size, self.max_blocks, cfg.max_model_len, self.part_o.data_ptr(),
-                         self.part_ml.data_ptr(), self.sample_scratch.data_ptr(), hidden=cfg.hidden)
-        g.single_rows = Hx.single_rows(ents, S)
+                         self.part_ml.data_ptr(), self.sample_scratch.data_ptr(), hidden=cfg.hidden,
+                         single_rows=single)
         d = self.device
         ids_ptr = self.meta_dev.data_ptr() + lay.ids
         H, nq, nkv, hd, F = cfg.hidden, cfg.n_head, cfg.n_kv_head, cfg.head_dim, cfg.ffn

@@ -1,4 +1,7 @@
-"""Per-step metadata the attention path consumes, restated from the reference executor.
+"""Per-step metadata the attention path consumes, restated from the reference executor in Python.
+
+The product path builds this metadata in C++ (``llmgen_fill_meta``, include/llmgen_host.h); this module is an
+independent restatement that the tests hold the C++ one against and that feeds the CPU oracle's inputs.
 
 * :func:`part_size` / :func:`max_parts` -- split-K part length and count (``attention_v1.zig:51-57``).
 * :func:`workspace_bytes` -- split-K scratch sizing (``executor.zig:92-102``).

@@ -55,6 +55,26 @@ class Workload:
                          seq_num=len(self.entries) + self.pad_rows, decode=self.decode)
 
     @property
+    def seq_num(self) -> int:
+        return len(self.entries) + self.pad_rows
+
+    def workspace(self, device="cuda"):
+        """The executor's attention workspace for this step (metadata buffer + split-K scratch)."""
+        from . import attention as A
+
+        return A.Workspace.allocate(self.nq, self.hd, max(self.seq_num, 1), self.max_model_len,
+                                    A.meta_bytes(self.entries, self.max_blocks, self.seq_num, self.decode),
+                                    device=device)
+
+    def bind(self, ws):
+        """fillMeta + upload + bindStep of this step through the C++ executor slice; returns (and publishes as
+        ``attention.g_step``) the bound StepState."""
+        from . import attention as A
+
+        return A.bind_step(self.entries, ws, self.nq, self.nkv, self.hd, self.block_size, self.max_blocks,
+                           self.max_model_len, seq_num=self.seq_num, decode=self.decode)
+
+    @property
     def n_tok(self) -> int:
         return sum(e.q_len for e in self.entries) + self.pad_rows
 

@@ -20,17 +20,15 @@ def check_hip_error(what: str) -> None:
 
 
 def run_gpu(wl: Workload, t: dict):
-    """store_kv + attention on the GPU via PagedAttentionImpl.  t: dict of bf16 device tensors (not modified).
+    """store_kv + attention on the GPU via PagedAttentionImpl (the C++ executor slice: fillMeta, bindStep,
+    llmgen_paged_attention).  t: dict of bf16 device tensors (not modified).
     Returns (out [T,nq,hd] bf16 device, kc, vc after the step)."""
     A.init_device()
-    pf = lib().hip_attn_prefill_tile()
-    meta = wl.meta(pf)
-    n_seq = meta.n_seq
-    ws = A.Workspace.allocate(wl.nq, wl.hd, max(n_seq, 1), wl.max_model_len, meta_elems=meta.packed().size)
+    ws = wl.workspace()
     mgr = A.PagedAttentionManager()
     mgr.layers[0] = A.LayerState(t["kc"].clone(), t["vc"].clone())
     A.g_attn_mgr = mgr
-    A.bind_step(meta, ws, wl.nq, wl.nkv, wl.hd, wl.block_size, wl.max_blocks, wl.max_model_len)
+    wl.bind(ws)
     out = torch.full((wl.n_tok, wl.nq, wl.hd), float("nan"), dtype=torch.bfloat16, device=t["q"].device)
     A.PagedAttentionImpl.execute(0, A.AttnNode(out, [t["q"], t["k"], t["v"]], layer_id=0))
     torch.cuda.synchronize()

@@ -184,30 +184,33 @@ def test_golden_vectors(gpu):
 
 
 def test_decode_graph_replays(gpu):
-    """executor.zig:541-575 replay semantics: one captured store_kv + decode bucket replayed with different
-    batches (all rows real, then 20 real + 12 padding rows, then all real again), with eager launches in
-    between; every replay is checked against the oracle."""
-    from llmgen_amd.graphs import DecodeGraphs
+    """executor.zig:541-575 replay semantics through the C++ graph buckets: one captured store_kv + decode bucket
+    replayed with different batches (all rows real, then 20 real + 12 padding rows, then all real again), with
+    eager launches in between; every replay is checked against the oracle and padding rows are zero."""
+    from llmgen_amd import host as H
 
     print("[gpu-test] decode graph replays", flush=True)
     wl = make("c2")
     t = wl.tensors(device="cuda")
-    layer = A.LayerState(t["kc"].clone(), t["vc"].clone())
-    graphs = DecodeGraphs(layer, wl.nq, wl.nkv, wl.hd, wl.block_size, wl.max_blocks, wl.max_model_len,
-                          max_seqs=32, buckets=[32])
+    kc, vc = t["kc"].clone(), t["vc"].clone()
+    graphs = H.Graphs([kc], [vc], wl.nq, wl.nkv, wl.hd, wl.block_size, wl.max_model_len, max_seqs=32, buckets=[32])
+    seqs = [H.Sequence_([0] * (e.q_start + e.q_len), list(e.block_table)) for e in wl.entries]
     try:
         for n in (32, 20, 32):
-            ents = wl.entries[:n]
-            sub = type(wl)(**{**wl.__dict__, "entries": ents})
-            b = graphs.prepare(ents, t["q"][:n], t["k"][:n], t["v"][:n])
-            graphs.launch(b)
+            ents = [(i, e.q_start, e.q_len) for i, e in enumerate(wl.entries[:n])]
+            sub = type(wl)(**{**wl.__dict__, "entries": wl.entries[:n]})
+            kc.copy_(t["kc"])
+            vc.copy_(t["vc"])
+            out = torch.full((32, wl.nq, wl.hd), float("nan"), dtype=torch.bfloat16, device="cuda")
+            used = graphs.step(seqs, ents, t["q"][:n], t["k"][:n], t["v"][:n], out)
+            assert used == 32
             torch.cuda.synchronize()
             check_hip_error(f"graph replay n={n}")
             ts = {"q": t["q"][:n], "k": t["k"][:n], "v": t["v"][:n], "kc": t["kc"], "vc": t["vc"]}
             okc, _, _, of = run_oracle(sub, ts)
-            compare(to_u16(b.out[:n]), of, f"graph replay n={n}")
-            if n < 32:
-                assert not to_u16(b.out[n:]).any(), "padding rows of the bucket must be zero"
+            compare(to_u16(out[:n]), of, f"graph replay n={n}")
+            assert_cache_equal(to_u16(kc), okc, f"graph replay K n={n}")
+            assert np.isnan(out[n:].float().cpu().numpy()).all(), "only the real rows are copied out"
             # eager work between replays (a different step through the same library)
             run_gpu(make("kt_decode"), make("kt_decode").tensors(device="cuda"))
     finally:
@@ -222,11 +225,11 @@ def test_mixed_step_graph_capture(gpu):
     t = wl.tensors(device="cuda")
     pf = lib().hip_attn_prefill_tile()
     meta = wl.meta(pf)
-    ws = A.Workspace.allocate(wl.nq, wl.hd, meta.n_seq, wl.max_model_len, meta_elems=meta.packed().size)
+    ws = wl.workspace()
     mgr = A.PagedAttentionManager()
     mgr.layers[0] = A.LayerState(t["kc"].clone(), t["vc"].clone())
     A.g_attn_mgr = mgr
-    A.bind_step(meta, ws, wl.nq, wl.nkv, wl.hd, wl.block_size, wl.max_blocks, wl.max_model_len)
+    wl.bind(ws)
     out = torch.zeros((wl.n_tok, wl.nq, wl.hd), dtype=torch.bfloat16, device="cuda")
     node = A.AttnNode(out, [t["q"], t["k"], t["v"]], layer_id=0)
     A.PagedAttentionImpl.execute(0, node)  # warm-up (module load) outside capture
@@ -470,11 +473,11 @@ def test_mixed_step_graph_replay(gpu, name):
     L = lib()
     meta = wl.meta(L.hip_attn_prefill_tile())
     assert not meta.decode and meta.single_rows() > 0
-    ws = A.Workspace.allocate(wl.nq, wl.hd, meta.n_seq, wl.max_model_len, meta_elems=meta.packed().size)
+    ws = wl.workspace()
     mgr = A.PagedAttentionManager()
     mgr.layers[0] = A.LayerState(t["kc"].clone(), t["vc"].clone())
     A.g_attn_mgr = mgr
-    A.bind_step(meta, ws, wl.nq, wl.nkv, wl.hd, wl.block_size, wl.max_blocks, wl.max_model_len)
+    wl.bind(ws)
     node_out = torch.full((wl.n_tok, wl.nq, wl.hd), float("nan"), dtype=torch.bfloat16, device="cuda")
     node = A.AttnNode(node_out, [t["q"], t["k"], t["v"]], layer_id=0)
     A.PagedAttentionImpl.execute(0, node)
@@ -510,11 +513,11 @@ def test_pure_prefill_graph_replay(gpu, name):
     L = lib()
     meta = wl.meta(L.hip_attn_prefill_tile())
     assert not meta.decode and meta.single_rows() == 0 and wl.nq // wl.nkv == 2
-    ws = A.Workspace.allocate(wl.nq, wl.hd, meta.n_seq, wl.max_model_len, meta_elems=meta.packed().size)
+    ws = wl.workspace()
     mgr = A.PagedAttentionManager()
     mgr.layers[0] = A.LayerState(t["kc"].clone(), t["vc"].clone())
     A.g_attn_mgr = mgr
-    A.bind_step(meta, ws, wl.nq, wl.nkv, wl.hd, wl.block_size, wl.max_blocks, wl.max_model_len)
+    wl.bind(ws)
     node_out = torch.full((wl.n_tok, wl.nq, wl.hd), float("nan"), dtype=torch.bfloat16, device="cuda")
     node = A.AttnNode(node_out, [t["q"], t["k"], t["v"]], layer_id=0)
     A.PagedAttentionImpl.execute(0, node)

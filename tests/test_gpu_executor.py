@@ -34,7 +34,7 @@ def _run_cpp(wl, t, seqs, entries, pf_tile, seq_num=None, max_blocks=None):
     n = len(entries)
     seq_num = n if seq_num is None else seq_num
     mb = wl.max_blocks if max_blocks is None else max_blocks
-    buf, lay, _ = H.fill_meta(seqs, entries, seq_num, n_tiles, pf_tile, wl.block_size, mb)
+    buf, lay, _, single = H.fill_meta(seqs, entries, seq_num, n_tiles, pf_tile, wl.block_size, mb)
     dev = t["q"].device
     meta_dev = torch.from_numpy(buf).to(dev)
     n_real = sum(e[2] for e in entries)
@@ -43,8 +43,8 @@ def _run_cpp(wl, t, seqs, entries, pf_tile, seq_num=None, max_blocks=None):
     po = torch.empty(ws["part_o"] // 4 + 1, dtype=torch.float32, device=dev)
     pml = torch.empty(ws["part_ml"] // 4 + 1, dtype=torch.float32, device=dev)
     st = H.bind_step(meta_dev.data_ptr(), lay, n_tok, seq_num, n_tiles, decode, wl.nq, wl.nkv, wl.hd,
-                     wl.block_size, mb, wl.max_model_len, po.data_ptr(), pml.data_ptr())
-    st.single_rows = H.single_rows(entries, seq_num)
+                     wl.block_size, mb, wl.max_model_len, po.data_ptr(), pml.data_ptr(), single_rows=single)
+    assert st.single_rows == H.single_rows(entries, seq_num)
     kc, vc = t["kc"].clone(), t["vc"].clone()
 
     def rows(x):

@@ -34,7 +34,7 @@ def test_fill_meta_matches_python_restatement_mixed_step():
     seqs, entries = _mixed()
     bs, mb, tile = 16, 10, 64
     n_tiles = sum((e[2] + tile - 1) // tile for e in entries)
-    buf, lay, seed = H.fill_meta(seqs, entries, len(entries), n_tiles, tile, bs, mb, step_seed=5)
+    buf, lay, seed, _ = H.fill_meta(seqs, entries, len(entries), n_tiles, tile, bs, mb, step_seed=5)
     n_tok = sum(e[2] for e in entries)
     seg = H.segments(buf, lay, n_tok, len(entries), n_tiles, mb)
     py = S.fill_meta([S.Entry(e[1], e[2], seqs[e[0]].block_table) for e in entries], bs, mb, tile,
@@ -52,7 +52,8 @@ def test_fill_meta_matches_python_restatement_mixed_step():
 def test_fill_meta_decode_bucket_padding():
     seqs = [H.Sequence_(list(range(100)), [2, 0], 0.0), H.Sequence_(list(range(11)), [1], 0.0)]
     entries = [(0, 99, 1), (1, 10, 1)]
-    buf, lay, _ = H.fill_meta(seqs, entries, 4, 0, 64, 64, 2)
+    buf, lay, _, single = H.fill_meta(seqs, entries, 4, 0, 64, 64, 2)
+    assert single == 4
     seg = H.segments(buf, lay, 4, 4, 0, 2)
     py = S.fill_meta([S.Entry(99, 1, [2, 0]), S.Entry(10, 1, [1])], 64, 2, 64, seq_num=4)
     for name in ("slots", "cu_q", "ctx", "last"):
@@ -60,7 +61,7 @@ def test_fill_meta_decode_bucket_padding():
     assert list(seg["slots"]) == [0 * 64 + 35, 1 * 64 + 10, -1, -1]
     assert list(seg["ids"]) == [99, 10, 0, 0] and not seg["block_tables"][2:].any()
     # the bucket layout does not depend on the entries: a step with fewer sequences reuses it
-    buf2, lay2, _ = H.fill_meta([], [], 4, 0, 64, 64, 2)
+    buf2, lay2, _, _ = H.fill_meta([], [], 4, 0, 64, 64, 2)
     assert lay2.as_dict() == lay.as_dict()
 
 
@@ -109,12 +110,34 @@ def test_single_rows_counts_one_row_segments():
     seqs, entries = _mixed()
     tile, bs, mb = 64, 16, 10
     n_tiles = sum((e[2] + tile - 1) // tile for e in entries)
-    buf, lay, _ = H.fill_meta(seqs, entries, len(entries), n_tiles, tile, bs, mb)
+    buf, lay, _, single = H.fill_meta(seqs, entries, len(entries), n_tiles, tile, bs, mb)
     seg = H.segments(buf, lay, sum(e[2] for e in entries), len(entries), n_tiles, mb)
     expect = int(np.count_nonzero(np.diff(seg["cu_q"]) == 1))
-    assert H.single_rows(entries, len(entries)) == expect
+    assert H.single_rows(entries, len(entries)) == expect == single
     py = S.fill_meta([S.Entry(e[1], e[2], seqs[e[0]].block_table) for e in entries], bs, mb, tile, decode=False)
     assert py.single_rows() == expect
     # padding rows of a bucket are one-row segments too
     assert H.single_rows([(0, 99, 1), (1, 10, 1)], 4) == 4
     assert H.single_rows([(0, 0, 70)], 1) == 0
+
+
+def test_fill_meta_prefill_padding_rows_get_tiles():
+    """A prefill step with padding rows (not an engine step, but legal): each padding row gets a tile, the tile
+    list (lightest first, padding rows first) equals the Python restatement's, and the single-row count covers
+    the padding rows; a tile count without room for them is rejected."""
+    seqs, entries = _mixed()
+    tile, bs, mb = 64, 16, 10
+    n_pad = 2
+    n_tiles = sum((e[2] + tile - 1) // tile for e in entries) + n_pad
+    seq_num = len(entries) + n_pad
+    buf, lay, _, single = H.fill_meta(seqs, entries, seq_num, n_tiles, tile, bs, mb)
+    n_tok = sum(e[2] for e in entries) + n_pad
+    seg = H.segments(buf, lay, n_tok, seq_num, n_tiles, mb)
+    py = S.fill_meta([S.Entry(e[1], e[2], seqs[e[0]].block_table) for e in entries], bs, mb, tile,
+                     seq_num=seq_num, decode=False)
+    for name in ("slots", "cu_q", "ctx", "last", "tile_seq", "tile_q0"):
+        np.testing.assert_array_equal(seg[name], getattr(py, name), err_msg=name)
+    assert single == py.single_rows() == H.single_rows(entries, seq_num)
+    assert set(seg["tile_seq"][:n_pad]) == {len(entries), len(entries) + 1}
+    with pytest.raises(ValueError):
+        H.fill_meta(seqs, entries, seq_num, n_tiles - 1, tile, bs, mb)

@@ -1,7 +1,8 @@
 """GPU: hip_attn_decode_noalloc (split-K partials in the library's own device array, no caller scratch, no
 allocation) gives bit for bit what hip_attn_decode gives with caller-owned scratch, on consecutive calls whose
-inputs shrink (so the second call finds the first call's partials in the shared array), and rejects a launch
-whose partials exceed the array without launching anything."""
+inputs shrink (so the second call finds the first call's partials in the shared array), runs single-part launches
+of any size without the array, and rejects a launch whose partials exceed the array without launching anything,
+reporting it through hip_last_error()."""
 from __future__ import annotations
 
 import numpy as np
@@ -57,18 +58,70 @@ def test_noalloc_decode_equals_caller_scratch_on_shrinking_calls(gpu):
         np.testing.assert_array_equal(got, ref, err_msg=f"noalloc != hip_attn_decode on {name}")
 
 
+def _custom(name, nq, nkv, bs, ctxs, seed):
+    """A decode step of len(ctxs) sequences with contiguous per-sequence blocks, as a named Workload."""
+    from llmgen_amd.workloads import Workload, _decode_entries, _tables
+
+    rng = np.random.default_rng(seed)
+    tables, nb = _tables(rng, ctxs, bs, permute=True)
+    mb = max(len(t) for t in tables)
+    return Workload(name, nq, nkv, 128, bs, nb, mb, mb * bs, _decode_entries(ctxs, tables), std=1.0, seed=seed)
+
+
+def _inputs_of(wl):
+    t = wl.tensors(device="cuda")
+    meta = wl.meta(64)
+    n = meta.n_tok
+    d = lambda a: torch.from_numpy(a).to("cuda")  # noqa: E731
+    kc, vc = t["kc"], t["vc"]
+    lib().hip_store_kv(t["k"].data_ptr(), t["v"].data_ptr(), d(meta.slots).data_ptr(), kc.data_ptr(),
+                       vc.data_ptr(), n, wl.nkv, wl.hd, wl.block_size)
+    return n, t["q"][:n].contiguous(), kc, vc, d(meta.block_tables), d(meta.ctx)
+
+
+def test_noalloc_decode_large_single_part_batch(gpu):
+    """512 sequences at 32 heads: one part per (sequence, head), so no partial is stored and the launch runs
+    whatever S * nq is (its partials at max_parts would exceed the array); equal to hip_attn_decode bit for bit."""
+    print("[gpu-test] noalloc 512x32 single part", flush=True)
+    rng = np.random.default_rng(61)
+    wl = _custom("big", 32, 8, 16, [int(c) for c in rng.integers(1, 120, size=512)], 61)
+    n, q, kc, vc, bt, ctx = _inputs_of(wl)
+    assert lib().hip_last_error() == 0
+    ref, got = _both(wl, n, q, kc, vc, bt, ctx)
+    np.testing.assert_array_equal(got, ref)
+
+
 def test_noalloc_decode_rejects_oversized_launch(gpu):
-    """A launch whose partials would need more than the array (20000 sequences, 16 heads) prints one line and
-    launches nothing: the output is untouched and no HIP error is raised."""
+    """One sequence of 65280 keys at GQA 16 (nkv 1) with 64-token parts and max_parts 1020: the launcher keeps
+    1020 parts (a 1-pair launch is far below one generation of workgroups), whose partials need
+    16 x 1020 x 520 B > 8 MiB.  The call prints one line, launches nothing (the output keeps its sentinel) and
+    hip_last_error() reports the rejection; hip_attn_decode with caller scratch runs the same launch.  All
+    buffers are real and sized for the launch, so a launch accepted by mistake stays in bounds."""
+    if torch.cuda.get_device_properties(0).multi_processor_count != 256:
+        pytest.skip("the part count of this launch is derived for 256 compute units")
     print("[gpu-test] noalloc oversized", flush=True)
-    out = torch.full((4, 16, 128), 3.0, dtype=torch.bfloat16, device="cuda")
-    before = to_u16(out).copy()
-    dummy = torch.zeros(1 << 12, dtype=torch.int32, device="cuda").data_ptr()
-    lib().hip_attn_decode_noalloc(out.data_ptr(), dummy, dummy, dummy, dummy, dummy, 20000, 16, 8, 128, 64, 256,
-                                  0.088, 512, 64)
+    L = lib()
+    wl = _custom("over", 16, 1, 256, [65280], 62)
+    n, q, kc, vc, bt, ctx = _inputs_of(wl)
+    ps, mp = 64, 1020
+    assert wl.max_blocks * wl.block_size >= ps * mp
+    common = (q.data_ptr(), kc.data_ptr(), vc.data_ptr(), bt.data_ptr(), ctx.data_ptr(), n, wl.nq, wl.nkv, wl.hd,
+              wl.max_blocks, wl.block_size, wl.scale)
     torch.cuda.synchronize()
-    check_hip_error("noalloc oversized")
+    assert L.hip_last_error() == 0
+    out = torch.full((n, wl.nq, wl.hd), 3.0, dtype=torch.bfloat16, device="cuda")
+    before = to_u16(out).copy()
+    L.hip_attn_decode_noalloc(out.data_ptr(), *common, ps, mp)
+    torch.cuda.synchronize()
+    assert L.hip_last_error() != 0, "the rejected launch must be reported"
+    assert L.hip_last_error() == 0, "the report is cleared by the read"
     np.testing.assert_array_equal(to_u16(out), before)
+    po = torch.empty(n * wl.nq * mp * wl.hd, dtype=torch.float32, device="cuda")
+    pml = torch.empty(n * wl.nq * mp * 2, dtype=torch.float32, device="cuda")
+    L.hip_attn_decode(out.data_ptr(), *common, po.data_ptr(), pml.data_ptr(), ps, mp)
+    torch.cuda.synchronize()
+    check_hip_error("decode of the launch noalloc rejects")
+    assert not np.array_equal(to_u16(out), before)
 
 
 def test_noalloc_decode_replays_from_a_graph(gpu):
