@@ -116,15 +116,19 @@ def test_c_parser_sees_the_reference_shaped_launchers():
 
 
 def test_execute_body_issues_the_operator_calls():
-    """PagedAttentionImpl.execute reads g_step / kvOf and issues store_kv + prefill, or the fused decode."""
+    """PagedAttentionImpl.execute reads g_step / kvOf and issues store_kv + prefill (with the single-row count), or
+    the fused decode."""
     src = open(os.path.join(ZIG, "attention_hip.zig")).read()
     body = src[src.index("pub const PagedAttentionImpl"):]
     assert "common.kvOf(out.layer_id)" in body and "common.g_step" in body
-    for call in ("hip_store_kv(", "hip_attn_prefill(", "hip_attn_decode_store_kv("):
+    for call in ("hip_store_kv(", "hip_attn_prefill_rows(", "hip_attn_decode_store_kv("):
         assert call in body, call
     assert "pub const FlashAttentionImpl = PagedAttentionImpl;" in src
-    # the decode call passes every argument the C declaration has
-    for name in ("hip_attn_decode_store_kv", "hip_store_kv", "hip_attn_prefill"):
+    # prefill passes the step's single-row count (read from g_step when the engine records it)
+    assert _call_args(body, "hip_attn_prefill_rows")[-1].strip() == "singleRowsOf(st)"
+    assert '@hasField(@TypeOf(st.*), "single_rows")' in src
+    # every call passes every argument the C declaration has
+    for name in ("hip_attn_decode_store_kv", "hip_store_kv", "hip_attn_prefill_rows"):
         assert len(_call_args(body, name)) == len(c_decls()[name][1]), name
 
 
@@ -148,3 +152,12 @@ def _call_args(src, name):
             cur += ch
     args.append(cur)
     return [a for a in args if a.strip()]
+
+
+def test_step_hints_zig_mirrors_the_cpp_fill_meta():
+    """zig/step_hints.zig (what the Zig executor adds to fillMeta / bindStep) has the two functions, with the
+    C++ slice's ordering key (keys a tile needs = ctx - q_len + min(q0 + tile, q_len)) and a stable sort."""
+    src = open(os.path.join(ZIG, "step_hints.zig")).read()
+    assert "pub fn singleRows(" in src and "pub fn sortTilesLightestFirst(" in src
+    assert "ctx[s] - q_len + tile_end" in src and "@min(tq0[i] + @as(i32, @intCast(pf_tile)), q_len)" in src
+    assert "> key" in src  # strictly greater: equal keys keep their order (stable)

@@ -7,7 +7,8 @@
 //! `common.kvOf(out.layer_id)`, exactly as the CUDA implementation reads them; the externs below are the C-ABI of
 //! include/llmgen_attn.h, each the hip_ counterpart of one cuda_ extern of attention_v1.zig:10-48.
 //!
-//! One difference in what is issued: a decode step (one query token per sequence) calls
+//! Prefill and mixed steps call hip_attn_prefill_rows (hip_attn_prefill plus the step's single-row count, which
+//! the executor records with step_hints.zig).  One more difference in what is issued: a decode step (one query token per sequence) calls
 //! hip_attn_decode_store_kv, which writes the step's K/V into the cache and attends in one launch; the CUDA path
 //! issues cuda_store_kv and then cuda_attn_decode.  Outputs and cache contents are the same.
 //! Not compiled in this repository (no Zig toolchain here); tests/test_zig_binding.py checks every extern
@@ -146,6 +147,13 @@ pub fn maxParts(s: usize, max_model_len: usize) usize {
     return (max_model_len + ps - 1) / ps;
 }
 
+/// The step's count of single-row segments, if the engine's StepState carries it (the `single_rows: c_int = -1`
+/// field that INTEGRATION.md adds to common.zig, set by bindStep from step_hints.singleRows), else -1.
+fn singleRowsOf(st: anytype) c_int {
+    if (@hasField(@TypeOf(st.*), "single_rows")) return st.single_rows;
+    return -1;
+}
+
 /// src[0] = q [1, T, nq, hd], src[1] = k [1, T, nkv, hd], src[2] = v [1, T, nkv, hd]; out.data = [1, T, nq, hd],
 /// all bf16.  Errors as the CUDA implementation: error.NoAttentionManager / error.LayerNotActive from kvOf.
 pub const PagedAttentionImpl = struct {
@@ -157,11 +165,12 @@ pub const PagedAttentionImpl = struct {
         const v = out.src[2].?.data;
 
         if (!st.decode) {
-            // prefill or mixed step: write the step's rows into the paged cache, then causal varlen attention
+            // prefill or mixed step: write the step's rows into the paged cache, then causal varlen attention with
+            // the step's single-row count (step_hints.zig; -1 = unknown when the executor does not record it)
             hip_store_kv(k, v, st.slots, layer.k, layer.v, st.n_tok, st.n_kv_head, st.head_dim, st.block_size);
-            hip_attn_prefill(out.data, q, layer.k, layer.v, st.block_tables, st.ctx, st.cu_q, st.tile_seq,
+            hip_attn_prefill_rows(out.data, q, layer.k, layer.v, st.block_tables, st.ctx, st.cu_q, st.tile_seq,
                 st.tile_q0, st.n_tiles, st.n_head, st.n_kv_head, st.head_dim, st.max_blocks, st.block_size,
-                st.attn_scale);
+                st.attn_scale, singleRowsOf(st));
             return;
         }
         // decode step (also the body of a captured graph bucket): KV write and split-K decode in one launch

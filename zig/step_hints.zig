@@ -1,0 +1,52 @@
+//! step_hints.zig -- the two facts about a step that the HIP prefill launcher uses and the engine's executor
+//! knows while it packs the step (src/executor.zig:772-861 fillMeta), written for that executor:
+//!
+//!   * singleRows: how many segments of the step have one query row (decode rows of a mixed step, and graph
+//!     padding rows).  hip_attn_prefill_rows takes it: 0 skips the launch that streams such rows (a grid of
+//!     workgroups that would find nothing to do) and lets small pure-prefill steps take the key-split kernel.
+//!   * sortTilesLightestFirst: reorder the packed prefill tiles by the number of keys each tile needs, lightest
+//!     first and stable.  The prefill kernel dispatches the list from its end, so the heaviest tiles (a long
+//!     prompt's last ones) start first and do not form the tail of the launch.  Any order is valid for the kernel;
+//!     this one is faster.
+//!
+//! Both are the C++ executor slice's behaviour (llmgen_amd/csrc/executor.cpp llmgen_fill_meta /
+//! llmgen_single_rows), restated for the Zig executor.  Neither allocates.  Not compiled in this repository (no Zig
+//! toolchain here).
+
+/// Segments with one query row: entries with q_len == 1, plus the seq_num - entries.len padding rows of a graph
+/// bucket.  `entries` is any slice whose elements have a `q_len` field (executor.zig's Entry).
+pub fn singleRows(entries: anytype, seq_num: usize) c_int {
+    var n: usize = if (seq_num > entries.len) seq_num - entries.len else 0;
+    for (entries) |e| {
+        if (e.q_len == 1) n += 1;
+    }
+    return @intCast(n);
+}
+
+/// Keys tile i needs: its sequence's context minus the rows after the tile.
+fn tileKeys(tseq: [*]const i32, tq0: [*]const i32, cu_q: [*]const i32, ctx: [*]const i32, pf_tile: usize, i: usize) i32 {
+    const s: usize = @intCast(tseq[i]);
+    const q_len = cu_q[s + 1] - cu_q[s];
+    const tile_end = @min(tq0[i] + @as(i32, @intCast(pf_tile)), q_len);
+    return ctx[s] - q_len + tile_end;
+}
+
+/// Stable insertion sort of the n_tiles packed tiles (tile_seq / tile_q0 segments of the metadata) by the keys
+/// each needs, lightest first.  Tiles of one sequence are already in increasing order, so the sort only
+/// interleaves sequences; a step has at most max_tokens / pf_tile + max_seqs tiles.
+pub fn sortTilesLightestFirst(tseq: [*]i32, tq0: [*]i32, n_tiles: usize, cu_q: [*]const i32, ctx: [*]const i32,
+    pf_tile: usize) void {
+    var i: usize = 1;
+    while (i < n_tiles) : (i += 1) {
+        const key = tileKeys(tseq, tq0, cu_q, ctx, pf_tile, i);
+        const s = tseq[i];
+        const q0 = tq0[i];
+        var j = i;
+        while (j > 0 and tileKeys(tseq, tq0, cu_q, ctx, pf_tile, j - 1) > key) : (j -= 1) {
+            tseq[j] = tseq[j - 1];
+            tq0[j] = tq0[j - 1];
+        }
+        tseq[j] = s;
+        tq0[j] = q0;
+    }
+}
