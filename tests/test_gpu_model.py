@@ -15,6 +15,8 @@
 """
 from __future__ import annotations
 
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -185,6 +187,15 @@ GREEDY_SEED = 3
 DECISIVE = 4.0  # a row-step is decisive when its top-2 margin exceeds this many two-ordering drifts
 
 
+def _record(name: str, lines) -> None:
+    """Keep a run's greedy-id evidence: written to <repo>/gpurun_out/<name> when that folder exists (a GPU box
+    run returns it), so the ids, margins and agreement counts survive ``pytest -q``."""
+    out_dir = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "gpurun_out")
+    if os.path.isdir(out_dir):
+        with open(os.path.join(out_dir, name), "w") as f:
+            f.write("\n".join(lines) + "\n")
+
+
 def _top2(lg_row: np.ndarray):
     f = O.bf16_to_f32(lg_row).astype(np.float64)
     i1 = int(np.argmax(f))
@@ -243,11 +254,15 @@ def test_qwen3_greedy_ids_match_cpu_backend(qwen_pair):
         ents = [S.Entry(pos[i], 1, tables[i]) for i in range(2)]
         ids_in = gen_c[-1]
         pos = [p + 1 for p in pos]
-    print(f"[qwen3] greedy ids cpu {gen_c}")
-    print(f"[qwen3] greedy ids gpu {gen_g}")
-    print(f"[qwen3] (top-2 margin, two-ordering drift) per step and row: {margins}")
-    print(f"[qwen3] logits vs CPU backend (max-abs, rel-L2) per step: {errs}")
-    print(f"[qwen3] floor: two-pass CPU attention vs CPU backend: {floors}")
+    rec = [f"teacher-forced greedy run (test_qwen3_greedy_ids_match_cpu_backend): prompts {lens}, 7 steps",
+           f"greedy ids cpu {gen_c}", f"greedy ids gpu {gen_g}",
+           f"(top-2 margin, two-ordering drift) per step and row: {margins}",
+           f"decisive row-steps: {decisive} of {7 * len(lens)} (margin > {DECISIVE} x drift)",
+           f"logits vs CPU backend (max-abs, rel-L2) per step: {errs}",
+           f"floor: two-pass CPU attention vs CPU backend: {floors}"]
+    for line in rec:
+        print("[qwen3] " + line)
+    _record("greedy_teacher_forced.txt", rec)
     check_err()
     distinct = len({i for step in gen_c for i in step})
     n_rows = 7 * len(lens)
@@ -255,6 +270,76 @@ def test_qwen3_greedy_ids_match_cpu_backend(qwen_pair):
     assert decisive >= n_rows * 2 // 3, f"only {decisive} of {n_rows} row-steps decisive: {margins}"
     for e, f in zip(errs, floors):
         assert e[1] <= 2 * f[1] + 1e-3, (errs, floors)
+
+
+@pytest.mark.timeout(900)
+def test_qwen3_free_running_greedy_ids_match_cpu_backend(qwen_pair):
+    """A fixed short free-running greedy run (models/qwen3.zig:165-330, cpu/sample.zig:37 at temperature 0): the
+    GPU forward and the CPU backend each feed back their own ids for 12 steps (a ragged two-prompt prefill, then
+    11 decode steps).  The rule, per row, while the two id sequences are still identical: a decisive step (CPU
+    top-2 margin > DECISIVE x the two-ordering drift of that step) must give the same id on both sides; a
+    non-decisive step (logits are bf16, so a margin of one or two bf16 ulps is common) may give another near-tied
+    id, and the first such difference ends what the row can be held to.  The test reports how many steps agree
+    exactly and requires at least 8 identical steps per row and at least 8 distinct ids, so that the run pins the
+    attention path over a real generation rather than one step."""
+    cfg, G, C, C2 = qwen_pair
+    mb = G.max_blocks
+    rng = np.random.default_rng(7)
+    lens = [29, 45]
+    tables = [list(rng.permutation(np.arange(0, 80))[:mb]), list(rng.permutation(np.arange(80, 160))[:mb])]
+    prompts = [rng.integers(0, cfg.vocab, n).tolist() for n in lens]
+    n_steps = 12
+    ents = [S.Entry(0, n, tables[i]) for i, n in enumerate(lens)]
+    in_g = in_c = sum(prompts, [])
+    gen_g, gen_c, margins = [], [], []
+    held = [True, True]  # the row's id sequences are still identical
+    first_tie = [None, None]  # the step at which a near tie parted the row's sequences
+    pos = list(lens)
+    for step in range(n_steps):
+        meta = S.fill_meta(ents, cfg.block_size, mb, G.pf_tile)
+        print(f"[qwen3-free] step {step} n_tok {meta.n_tok} decode {meta.decode}", flush=True)
+        ids_g = [int(i) for i in G.forward(ents, in_g, fused_qk=(step % 2 == 1))]
+        ids_c, lg_c = C.forward(meta, in_c, mb, return_logits=True)
+        _, lg_c2 = C2.forward(meta, in_c, mb, return_logits=True)
+        ids_c = [int(i) for i in ids_c]
+        gen_g.append(ids_g)
+        gen_c.append(ids_c)
+        row_m = []
+        for r in range(len(lens)):
+            fc, ic, margin = _top2(lg_c[r])
+            drift = float(np.sqrt(np.mean((O.bf16_to_f32(lg_c2[r]).astype(np.float64) - fc) ** 2)))
+            row_m.append((round(margin, 4), round(drift, 4)))
+            assert ic == ids_c[r]
+            if not held[r]:
+                continue
+            if margin > DECISIVE * drift:
+                assert ids_g[r] == ic, (f"free run step {step} row {r}: gpu {ids_g[r]} cpu {ic}, margin "
+                                        f"{margin:.4g} > {DECISIVE} x drift {drift:.4g}; ids gpu {gen_g} cpu {gen_c}")
+            elif ids_g[r] != ic:  # a near tie went the other way: the sequences part here
+                first_tie[r] = step
+                held[r] = False
+        margins.append(row_m)
+        ents = [S.Entry(pos[i], 1, tables[i]) for i in range(2)]
+        in_g, in_c = ids_g, ids_c
+        pos = [p + 1 for p in pos]
+    identical = [sum(1 for s in range(n_steps) if all(gen_g[t][r] == gen_c[t][r] for t in range(s + 1)))
+                 for r in range(len(lens))]
+    rec = [f"free-running greedy run (test_qwen3_free_running_greedy_ids_match_cpu_backend): prompts {lens}, "
+           f"{n_steps} steps, each side feeding back its own ids",
+           f"greedy ids cpu {gen_c}", f"greedy ids gpu {gen_g}",
+           f"(top-2 margin, two-ordering drift) per step and row: {margins}",
+           f"steps with identical id sequences so far, per row: {identical} of {n_steps}",
+           f"step at which a near tie parted the sequences, per row (None = never): {first_tie}",
+           f"non-decisive row-steps (margin <= {DECISIVE} x drift) while identical: "
+           f"{[[t for t in range(n_steps) if margins[t][r][0] <= DECISIVE * margins[t][r][1]] for r in range(len(lens))]}"]
+    for line in rec:
+        print("[qwen3-free] " + line)
+    _record("greedy_free_running.txt", rec)
+    check_err()
+    distinct = len({i for step in gen_c for i in step})
+    assert distinct >= 8, f"ids barely change ({distinct} distinct): {gen_c}"
+    for r in range(len(lens)):
+        assert identical[r] >= 8, f"row {r}: only {identical[r]} identical steps ({margins})"
 
 
 @pytest.mark.parametrize("T,nq,nkv,bs,nb", [(32, 16, 8, 256, 40), (300, 32, 8, 16, 64), (5, 16, 16, 16, 8)])
