@@ -144,9 +144,11 @@ int llmgen_fill_meta(uint8_t *meta_host, llmgen_layout lay, const llmgen_seq *se
             ++tile;
         }
     }
-    // Tiles lightest first, by the keys a tile needs (stable: entry order among equals).  The reference lists them
-    // in entry order; the prefill kernel accepts any order and dispatches the list from its end, so this makes
-    // its dispatch heaviest first across sequences (a long prompt's last tiles start before short prompts).
+    // Single-row tiles (decode and padding rows) first, then the multi-row tiles; each part lightest first, by the
+    // keys a tile needs (stable: entry order among equals).  The reference lists tiles in entry order.  The kernels
+    // accept any order: they walk each part from its end, so the longest decode rows and the heaviest prefill
+    // tiles (a long prompt's last ones) start first, and the single-row count hip_attn_prefill_rows takes marks
+    // where the parts meet.
     if (tile > 1) {
         std::vector<int> order(tile);
         std::vector<int32_t> kend(tile), s0(tseq, tseq + tile), q00(tq0, tq0 + tile);
@@ -155,7 +157,11 @@ int llmgen_fill_meta(uint8_t *meta_host, llmgen_layout lay, const llmgen_seq *se
             kend[i] = ctx[si] - q_len + std::min(q00[i] + pf_tile, q_len);
             order[i] = i;
         }
-        std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return kend[a] < kend[b]; });
+        std::vector<char> multi(tile);
+        for (int i = 0; i < tile; ++i) multi[i] = cu_q[s0[i] + 1] - cu_q[s0[i]] > 1;
+        std::stable_sort(order.begin(), order.end(), [&](int a, int b) {
+            return multi[a] != multi[b] ? multi[a] < multi[b] : kend[a] < kend[b];
+        });
         for (int i = 0; i < tile; ++i) {
             tseq[i] = s0[order[i]];
             tq0[i] = q00[order[i]];

@@ -88,6 +88,13 @@ __attribute__((visibility("hidden"))) void llmgen_decode_rows_of_prefill(
                                    const int *tile_seq, int n_tiles, int nq, int nkv, int max_blocks,
                                    int block_size, float scale, hipStream_t stream);
 
+// Internal: a mixed step (single_rows > 0 single-row segments listed first, then prefill tiles) as one launch of
+// the mixed-step kernel (mixed.hip); false if the shape is not one it takes (then nothing is launched).
+__attribute__((visibility("hidden"))) bool llmgen_mixed_step(
+    bf16_t *out, const bf16_t *q, const bf16_t *k_cache, const bf16_t *v_cache, const int *block_tables,
+    const int *ctx_lens, const int *cu_q, const int *tile_seq, const int *tile_q0, int n_tiles, int single_rows,
+    int nq, int nkv, int max_blocks, int block_size, float scale, int dma_mode);
+
 // Internal: fork onto / join back from the library's side stream (hip_context.hip).  Used to run independent
 // kernels of one launcher concurrently; legal inside stream capture.
 __attribute__((visibility("hidden"))) hipStream_t llmgen_fork_side_stream();

@@ -111,8 +111,9 @@ class StepMeta:
 
 def fill_meta(entries: Sequence[Entry], block_size: int, max_blocks: int, pf_tile: int,
               seq_num: Optional[int] = None, decode: Optional[bool] = None) -> StepMeta:
-    """executor.zig:530-552 + 772-861, except that prefill tiles are listed lightest first (stable) rather than in
-    entry order, so that the kernel's last-first dispatch is heaviest first.
+    """executor.zig:530-552 + 772-861, except that prefill tiles are listed single-row tiles first, then multi-row
+    ones, each part lightest first (stable), rather than in entry order, so that the kernels' last-first dispatch is
+    longest / heaviest first.
 
     ``decode`` defaults to the engine's rule (every entry has q_len == 1 and emits).  ``seq_num`` >= len(entries)
     adds padding rows (one token each, ctx = 0, slot = -1, zero block-table row) as for a graph bucket.  Prefill
@@ -168,10 +169,11 @@ def fill_meta(entries: Sequence[Entry], block_size: int, max_blocks: int, pf_til
         ctx[si] = 0
         last[si] = t - 1
     if n_tiles > 1:
-        # lightest first by the keys a tile needs (stable); the kernel dispatches the list from its end
+        # single-row tiles first, then multi-row ones, each part lightest first by the keys a tile needs (stable);
+        # the kernels walk each part from its end
         q_lens = np.diff(cu_q)[tile_seq]
         kend = ctx[tile_seq] - q_lens + np.minimum(tile_q0 + pf_tile, q_lens)
-        order = np.argsort(kend, kind="stable")
+        order = np.lexsort((kend, q_lens > 1))
         tile_seq, tile_q0 = tile_seq[order].copy(), tile_q0[order].copy()
     return StepMeta(n_tok=n_tok, n_seq=n_seq, n_tiles=n_tiles, decode=decode, slots=slots, cu_q=cu_q, ctx=ctx,
                     last=last, tile_seq=tile_seq, tile_q0=tile_q0, block_tables=bt, pos=posv)

@@ -156,8 +156,10 @@ def _call_args(src, name):
 
 def test_step_hints_zig_mirrors_the_cpp_fill_meta():
     """zig/step_hints.zig (what the Zig executor adds to fillMeta / bindStep) has the two functions, with the
-    C++ slice's ordering key (keys a tile needs = ctx - q_len + min(q0 + tile, q_len)) and a stable sort."""
+    C++ slice's ordering key (single-row tiles first, then keys a tile needs = ctx - q_len + min(q0 + tile,
+    q_len)) and a stable sort."""
     src = open(os.path.join(ZIG, "step_hints.zig")).read()
     assert "pub fn singleRows(" in src and "pub fn sortTilesLightestFirst(" in src
     assert "ctx[s] - q_len + tile_end" in src and "@min(tq0[i] + @as(i32, @intCast(pf_tile)), q_len)" in src
+    assert "(multi << 32) + keys" in src  # single-row tiles first
     assert "> key" in src  # strictly greater: equal keys keep their order (stable)
