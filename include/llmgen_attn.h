@@ -92,18 +92,35 @@ void hip_attn_prefill(uint16_t *out, const uint16_t *q, const uint16_t *k_cache,
                       int max_blocks, int block_size, float scale);
 
 /* hip_attn_prefill for a caller that knows how many segments of the step have one query row (the decode rows of
- * a mixed step, and padding rows): single_rows == 0 skips the launch that serves such rows, > 0 runs it, < 0
- * means unknown and behaves as hip_attn_prefill.  No reference counterpart (the reference kernel runs decode rows
- * as one-row prefill tiles); the executor slice (llmgen_paged_attention) passes the count it has from its
- * entries, so a pure prefill step does not pay for a grid of workgroups that find nothing to do.  The count must be
- * exact when it is 0: a step that has single-row segments but is passed 0 leaves those rows unwritten (pass -1
- * when unsure).  For GQA >= 2 a count of 0 also selects, on steps of at most 2.5 (query tile, KV head, head pair)
- * units per CU, the key-split prefill kernel, whose outputs differ from hip_attn_prefill's in the last bits (another
- * summation order, same tolerance). */
+ * a mixed step, and padding rows): single_rows == 0 skips the work that serves such rows, > 0 runs it, < 0 means
+ * unknown and behaves as hip_attn_prefill.  No reference counterpart (the reference kernel runs decode rows as
+ * one-row prefill tiles); the executor slice (llmgen_paged_attention) passes the count llmgen_fill_meta returned.
+ * The count must be exact when it is 0: a step that has single-row segments but is passed 0 leaves those rows
+ * unwritten (pass -1 when unsure).  With a count > 0 at G = 2 or 4 the whole step is one launch in which workgroups
+ * take either a prefill unit or a decode row; it is fastest when the list holds the single-row tiles first (as
+ * llmgen_fill_meta orders it) and gives the same result for any order.  For GQA >= 2 a count of 0 also selects,
+ * on steps of at most 2.5 (query tile, KV head, head pair) units per CU, the key-split prefill kernel.  Which
+ * kernel runs (hip_attn_prefill_plan) changes the summation order, so the same rows computed in steps of different
+ * composition or with a different count can differ in their last bits (same tolerance); one call is always
+ * bit-reproducible. */
 void hip_attn_prefill_rows(uint16_t *out, const uint16_t *q, const uint16_t *k_cache, const uint16_t *v_cache,
                            const int32_t *block_tables, const int32_t *ctx_lens, const int32_t *cu_q,
                            const int32_t *tile_seq, const int32_t *tile_q0, int n_tiles, int nq, int nkv, int hd,
                            int max_blocks, int block_size, float scale, int single_rows);
+
+/* No reference counterpart; for tests and tuning.  The launch hip_attn_prefill_rows makes for a step of this shape
+ * (n_tiles tiles, single_rows as passed to it): one LLMGEN_PREFILL_* kernel value, plus LLMGEN_PREFILL_ROWS_LAUNCH
+ * when a separate decode-row launch also runs on the library's side stream.  0 = nothing is launched (n_tiles <= 0),
+ * -1 = unsupported shape.  The choice depends only on these integers and the device's compute-unit count. */
+enum {
+    LLMGEN_PREFILL_MIXED = 1,     /* mixed step in one launch: prefill units and decode rows as workgroup roles */
+    LLMGEN_PREFILL_KEYSPLIT = 2,  /* 8-wave workgroups, two heads, key tiles split over two groups of 4 waves */
+    LLMGEN_PREFILL_W2 = 3,        /* 2-wave workgroups, one head (G = 1) */
+    LLMGEN_PREFILL_W4 = 4,        /* 4-wave workgroups, two heads */
+    LLMGEN_PREFILL_W8 = 5,        /* 8-wave workgroups, four heads */
+    LLMGEN_PREFILL_ROWS_LAUNCH = 16
+};
+int hip_attn_prefill_plan(int n_tiles, int nq, int nkv, int hd, int block_size, int single_rows);
 
 /* Replaces cuda_attn_prefill_tile (attention_v1.zig:48): query rows per prefill tile (64). */
 int hip_attn_prefill_tile(void);

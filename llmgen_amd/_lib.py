@@ -27,6 +27,7 @@ SIGNATURES = {
     "hip_attn_prefill": (None, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F]),
     "hip_attn_prefill_rows": (None, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _I]),
     "hip_attn_prefill_tile": (_I, []),
+    "hip_attn_prefill_plan": (_I, [_I, _I, _I, _I, _I, _I]),
     "hip_attn_set_option": (_I, [_I, _I]),
     "hip_init": (_I, [_SZ]),
     "hip_sync": (None, []),

@@ -87,6 +87,62 @@ void launch_prefill(int mode, int head_groups, bf16_t *out, const bf16_t *q, con
 
 extern "C" int hip_attn_prefill_tile(void) { return BQ; }
 
+namespace {
+
+// The launch hip_attn_prefill_rows makes for a step of this shape (hip_attn_prefill_plan reports it).
+struct PrefillPlan {
+    int kernel = 0;          // LLMGEN_PREFILL_* of llmgen_attn.h; 0 = nothing to launch
+    int heads_per_wg = 0;    // query heads per prefill workgroup (two waves each)
+    bool rows_launch = false;  // a separate decode-row launch on the side stream
+};
+
+PrefillPlan plan_prefill(int n_tiles, int G, int nkv, int single_rows) {
+    PrefillPlan p;
+    if (n_tiles <= 0) return p;
+    // A mixed step whose single-row count the caller knows runs as one launch (mixed.hip) at G = 2 and 4.
+    if (single_rows > 0 && (G == 2 || G == 4) && single_rows <= n_tiles) {
+        p.kernel = LLMGEN_PREFILL_MIXED;
+        p.heads_per_wg = 2;
+        return p;
+    }
+    // two waves per head; at most 8 waves (4 heads) per workgroup, the rest of the group in further workgroups
+    p.heads_per_wg = G < 4 ? G : 4;
+    // A small pure-prefill step at G >= 4 runs as G / 2 two-head groups so that it can take the key-split
+    // workgroups below (single G = 4 prompt of 2048 tokens: 47 against 57 us; at 3584 tokens, 896 units, the
+    // 8-wave four-head workgroups stay faster: 105 against 112-122 us)
+    if (single_rows == 0 && G >= 4 && (long)n_tiles * nkv * (G / 2) * 2 <= 5L * llmgen_num_cus()) p.heads_per_wg = 2;
+    const int head_groups = G / p.heads_per_wg;
+    // Decode rows (q_len == 1) of other mixed steps go to the bandwidth-oriented decode kernel on the side stream,
+    // concurrently with the MFMA kernel (which skips them).  Its grid covers every tile (which tiles are single rows
+    // is device data), so it is skipped when the caller knows there are none.
+    p.rows_launch = single_rows != 0;
+    if (p.heads_per_wg == 1) {
+        p.kernel = LLMGEN_PREFILL_W2;
+    } else if (p.heads_per_wg == 2) {
+        // Pure prefill of up to 2.5 units per CU: 8-wave workgroups whose two key groups split each unit's key
+        // tiles, so the heaviest units (a long prompt's last tiles) take half as many iterations (measured on
+        // single prompts: 64 against 75 us at 3584 tokens, even at 4608).  Larger steps are bound by throughput,
+        // where the 4-wave workgroups (two per CU) are faster (5632 tokens: 137 against 148 us; 16384: 986 against
+        // 1069 us).  With decode rows beside it a 128 KB workgroup finds no room next to the decode kernel's waves.
+        p.kernel = single_rows == 0 && (long)n_tiles * nkv * head_groups * 2 <= 5L * llmgen_num_cus()
+                       ? LLMGEN_PREFILL_KEYSPLIT
+                       : LLMGEN_PREFILL_W4;
+    } else {
+        p.kernel = LLMGEN_PREFILL_W8;
+    }
+    return p;
+}
+
+}  // namespace
+
+extern "C" int hip_attn_prefill_plan(int n_tiles, int nq, int nkv, int hd, int block_size, int single_rows) {
+    if (hd != HD || nkv <= 0 || nq <= 0 || nq % nkv != 0 || block_size <= 0) return -1;
+    const int G = nq / nkv;
+    if (G != 1 && G != 2 && G != 4 && G != 8 && G != 16) return -1;
+    const PrefillPlan p = plan_prefill(n_tiles, G, nkv, single_rows);
+    return p.kernel | (p.rows_launch ? LLMGEN_PREFILL_ROWS_LAUNCH : 0);
+}
+
 extern "C" void hip_attn_prefill_rows(bf16_t *out, const bf16_t *q, const bf16_t *k_cache,
                                       const bf16_t *v_cache, const int *block_tables, const int *ctx_lens,
                                       const int *cu_q, const int *tile_seq, const int *tile_q0, int n_tiles, int nq,
@@ -109,48 +165,36 @@ extern "C" void hip_attn_prefill_rows(bf16_t *out, const bf16_t *q, const bf16_t
     const int bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz(block_size) : -1;
     const int mode = (bs_shift >= 0 && block_size % BK == 0) ? DMA_BLOCK : (block_size % 4 == 0 ? DMA_ROW4 : DMA_FLAT);
     const float sl2 = scale * LLMGEN_LOG2E;
-    // A mixed step whose single-row count the caller knows runs as one launch (mixed.hip) at G = 2 and 4.
-    if (single_rows > 0 && llmgen_mixed_step(out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq,
-                                             tile_q0, n_tiles, single_rows, nq, nkv, max_blocks, block_size, scale,
-                                             mode))
+    const PrefillPlan plan = plan_prefill(n_tiles, G, nkv, single_rows);
+    if (plan.kernel == LLMGEN_PREFILL_MIXED) {
+        llmgen_mixed_step(out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq, tile_q0, n_tiles,
+                          single_rows, nq, nkv, max_blocks, block_size, scale, mode);
         return;
-    // two waves per head; at most 8 waves (4 heads) per workgroup, the rest of the group in further workgroups
-    int heads_per_wg = G < 4 ? G : 4;
-    // A small pure-prefill step at G >= 4 runs as G / 2 two-head groups so that it can take the key-split
-    // workgroups below (single G = 4 prompt of 2048 tokens: 47 against 57 us; at 3584 tokens, 896 units, the
-    // 8-wave four-head workgroups stay faster: 105 against 112-122 us)
-    if (single_rows == 0 && G >= 4 && (long)n_tiles * nkv * (G / 2) * 2 <= 5L * llmgen_num_cus()) heads_per_wg = 2;
-    const int head_groups = G / heads_per_wg;
-    // Decode rows (q_len == 1) go to the bandwidth-oriented decode kernel on the side stream, concurrently with
-    // the MFMA kernel (which skips them) on the launch stream: HBM-bound and MFMA-bound work overlap.  Its grid
-    // covers every tile (which tiles are single rows is device data), so it is skipped when the caller knows
-    // there are none: idle workgroups still take dispatch slots from the prefill kernel.
+    }
+    const int head_groups = G / plan.heads_per_wg;
     hipStream_t side = g_llmgen_stream;
-    if (single_rows != 0) {
+    if (plan.rows_launch) {
         side = llmgen_fork_side_stream();
         llmgen_decode_rows_of_prefill(out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq, n_tiles, nq,
                                       nkv, max_blocks, block_size, scale, side);
     }
-    switch (heads_per_wg) {
-        case 1: launch_prefill<2>(mode, head_groups, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq,
-                                  tile_q0, n_tiles, nq, nkv, G, max_blocks, block_size, bs_shift, sl2); break;
-        case 2:
-            // Pure prefill of up to 2.5 units per CU: 8-wave workgroups whose two key groups split each unit's key
-            // tiles, so the heaviest units (a long prompt's last tiles) take half as many iterations (c3 -7 %;
-            // measured on single prompts: 64 against 75 us at 3584 tokens, even at 4608).  Larger steps are
-            // bound by throughput, where the 4-wave workgroups (two per CU) are faster (5632 tokens: 137 against
-            // 148 us; 16384: 986 against 1069 us).  With decode rows beside it (single_rows != 0) a 128 KB
-            // workgroup finds no room next to the decode kernel's waves, and 4-wave workgroups are faster (c4 +9 %
-            // otherwise).
-            if (single_rows == 0 && (long)n_tiles * nkv * head_groups * 2 <= 5L * llmgen_num_cus())
-                launch_prefill<8, 2>(mode, head_groups, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q,
-                                     tile_seq, tile_q0, n_tiles, nq, nkv, G, max_blocks, block_size, bs_shift, sl2);
-            else
-                launch_prefill<4>(mode, head_groups, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q,
-                                  tile_seq, tile_q0, n_tiles, nq, nkv, G, max_blocks, block_size, bs_shift, sl2);
+    switch (plan.kernel) {
+        case LLMGEN_PREFILL_W2:
+            launch_prefill<2>(mode, head_groups, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq,
+                              tile_q0, n_tiles, nq, nkv, G, max_blocks, block_size, bs_shift, sl2);
             break;
-        default: launch_prefill<8>(mode, head_groups, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq,
-                                   tile_q0, n_tiles, nq, nkv, G, max_blocks, block_size, bs_shift, sl2); break;
+        case LLMGEN_PREFILL_KEYSPLIT:
+            launch_prefill<8, 2>(mode, head_groups, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq,
+                                 tile_q0, n_tiles, nq, nkv, G, max_blocks, block_size, bs_shift, sl2);
+            break;
+        case LLMGEN_PREFILL_W4:
+            launch_prefill<4>(mode, head_groups, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq,
+                              tile_q0, n_tiles, nq, nkv, G, max_blocks, block_size, bs_shift, sl2);
+            break;
+        default:
+            launch_prefill<8>(mode, head_groups, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq,
+                              tile_q0, n_tiles, nq, nkv, G, max_blocks, block_size, bs_shift, sl2);
+            break;
     }
     llmgen_join_side_stream(side);
 }

@@ -353,9 +353,11 @@ def test_zero_sized_launches_are_noops(gpu):
 @pytest.mark.parametrize("name", ["cpu_mixed", "bs48", "bs6", "gqa8", "c4", "c3", "kt_prefill"])
 def test_prefill_rows_hint_matches_unknown_count(gpu, name):
     """hip_attn_prefill_rows with the step's single-row segment count against hip_attn_prefill (count unknown).
-    With a count > 0 the same kernels run: bit-identical.  With 0 (a pure prefill step: no decode-row launch) a
-    small step of GQA >= 2 runs the key-split prefill kernel instead, which sums the keys in another order: both
-    outputs are checked against the oracle (sampled rows); GQA 1 stays bit-identical."""
+    With a count > 0 the step runs as one launch of the mixed-step kernel at GQA 2 and 4 (cpu_mixed, bs48, bs6, c4)
+    and as the same two kernels otherwise (gqa8): bit-identical either way, since every workgroup role computes its
+    rows as the separate kernels do.  With 0 (a pure prefill step: no decode-row launch) a small step of GQA >= 2
+    runs the key-split prefill kernel instead, which sums the keys in another order: both outputs are checked
+    against the oracle (sampled rows); GQA 1 stays bit-identical."""
     wl = make(name)
     print(f"[gpu-test] {name}", flush=True)
     t = wl.tensors(device="cuda")
@@ -387,6 +389,73 @@ def test_prefill_rows_hint_matches_unknown_count(gpu, name):
             compare(o[rows], of, f"{name} {what}")
     else:
         np.testing.assert_array_equal(outs[1], outs[0])
+
+
+def test_prefill_plan_names_the_kernel_each_config_runs(gpu):
+    """hip_attn_prefill_plan reports the launch hip_attn_prefill_rows makes, from the same rule: mixed steps at
+    GQA 2 / 4 with a known single-row count run one mixed-step launch, c3 (99 tiles x 8 KV heads = 792 units of two
+    heads, above 2.5 per CU) the 4-wave kernel, c5p (GQA 4, 256 tiles) the 8-wave four-head kernel, the small
+    pure prefills the key-split kernel, and an unknown count adds the separate decode-row launch."""
+    L = lib()
+    pf = L.hip_attn_prefill_tile()
+    plan = {}
+    for name in ("c3", "c4", "c5p", "kt_prefill", "gqa8", "gqa1", "cpu_mixed", "bs48"):
+        wl = make(name)
+        m = wl.meta(pf)
+        plan[name] = (L.hip_attn_prefill_plan(m.n_tiles, wl.nq, wl.nkv, wl.hd, wl.block_size, m.single_rows()),
+                      L.hip_attn_prefill_plan(m.n_tiles, wl.nq, wl.nkv, wl.hd, wl.block_size, -1))
+    MIXED, KEYSPLIT, W2, W4, W8, ROWS = 1, 2, 3, 4, 5, 16
+    assert plan["c3"] == (W4, W4 | ROWS)
+    assert plan["c4"] == (MIXED, W4 | ROWS)
+    assert plan["c5p"] == (W8, W8 | ROWS)
+    assert plan["kt_prefill"] == (KEYSPLIT, W4 | ROWS)
+    assert plan["gqa8"] == (W8 | ROWS, W8 | ROWS)
+    assert plan["gqa1"] == (W2 | ROWS, W2 | ROWS)
+    assert plan["cpu_mixed"][0] == MIXED and plan["bs48"][0] == MIXED
+    assert L.hip_attn_prefill_plan(0, 16, 8, 128, 256, 0) == 0
+    assert L.hip_attn_prefill_plan(4, 16, 8, 64, 256, 0) == -1 and L.hip_attn_prefill_plan(4, 24, 8, 128, 256, 0) == -1
+
+
+@pytest.mark.parametrize("name", ["c4", "bs48", "cpu_mixed"])
+def test_mixed_kernel_gives_the_same_rows_for_any_tile_order(gpu, name):
+    """The mixed-step kernel sizes its two parts from the single-row count and expects the single-row tiles first;
+    a list in any other order (here a seeded shuffle, which puts multi-row tiles in the decode part and single-row
+    tiles in the prefill part) must give the same output bit for bit, every role running whatever tile it finds."""
+    wl = make(name)
+    print(f"[gpu-test] mixed any order {name}", flush=True)
+    t = wl.tensors(device="cuda")
+    L = lib()
+    meta = wl.meta(L.hip_attn_prefill_tile())
+    assert not meta.decode and meta.single_rows() > 0
+    assert L.hip_attn_prefill_plan(meta.n_tiles, wl.nq, wl.nkv, wl.hd, wl.block_size, meta.single_rows()) == 1
+    kc, vc = t["kc"].clone(), t["vc"].clone()
+    outs = []
+    for shuffle in (False, True):
+        buf = meta.packed().copy()
+        if shuffle:
+            perm = np.random.default_rng(9).permutation(meta.n_tiles)
+            o_s, o_q = meta.offsets["tile_seq"], meta.offsets["tile_q0"]
+            buf[o_s:o_s + meta.n_tiles] = meta.tile_seq[perm]
+            buf[o_q:o_q + meta.n_tiles] = meta.tile_q0[perm]
+            moved = np.diff(meta.cu_q)[meta.tile_seq[perm]][:meta.single_rows()]
+            assert (moved > 1).any(), "the shuffle must put multi-row tiles into the decode part"
+        seg = torch.from_numpy(buf).to("cuda")
+        off = {k: seg.data_ptr() + 4 * v for k, v in meta.offsets.items()}
+        if not shuffle:
+            L.hip_store_kv(t["k"].data_ptr(), t["v"].data_ptr(), off["slots"], kc.data_ptr(), vc.data_ptr(),
+                           wl.n_tok, wl.nkv, wl.hd, wl.block_size)
+        out = torch.full((wl.n_tok, wl.nq, wl.hd), float("nan"), dtype=torch.bfloat16, device="cuda")
+        L.hip_attn_prefill_rows(out.data_ptr(), t["q"].data_ptr(), kc.data_ptr(), vc.data_ptr(), off["block_tables"],
+                                off["ctx"], off["cu_q"], off["tile_seq"], off["tile_q0"], meta.n_tiles, wl.nq, wl.nkv,
+                                wl.hd, wl.max_blocks, wl.block_size, wl.scale, meta.single_rows())
+        torch.cuda.synchronize()
+        check_hip_error(f"{name} shuffle={shuffle}")
+        outs.append(to_u16(out))
+    assert not np.isnan(oracle.bf16_to_f32(outs[0])).any()
+    np.testing.assert_array_equal(outs[1], outs[0])
+    if name != "c4":  # small steps: every row against the oracle as well
+        _, _, _, of = run_oracle(wl, t)
+        compare(outs[1], of, f"{name} shuffled")
 
 
 @pytest.mark.parametrize("name", ["kt_prefill", "cpu_mixed", "c2", "gqa8d", "bs48", "bs6", "c3"])

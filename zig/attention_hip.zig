@@ -131,6 +131,10 @@ pub extern fn hip_attn_prefill_rows(
 
 pub extern fn hip_attn_prefill_tile() c_int;
 
+/// The launch hip_attn_prefill_rows makes for a step of this shape (tests and tuning; no cuda_ counterpart).
+pub extern fn hip_attn_prefill_plan(n_tiles: c_int, nq: c_int, nkv: c_int, hd: c_int, block_size: c_int,
+    single_rows: c_int) c_int;
+
 pub extern fn hip_attn_set_option(option: c_int, value: c_int) c_int;
 
 /// Split-K part length and part count the engine sizes its scratch with (attention_v1.zig:51-57, unchanged:
