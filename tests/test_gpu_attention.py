@@ -573,8 +573,9 @@ def test_mixed_step_graph_replay(gpu, name):
 
 @pytest.mark.parametrize("name", ["c3", "kt_prefill"])
 def test_pure_prefill_graph_replay(gpu, name):
-    """A pure prefill step at GQA 2 (the key-split kernel, no decode-row launch) captured into a graph: three
-    replays with eager torch work between them each give the eager step's output bit for bit."""
+    """A pure prefill step at GQA 2 (no decode-row launch) captured into a graph: three replays with eager torch
+    work between them each give the eager step's output bit for bit.  c3 (792 two-head units, above the key-split
+    rule's 2.5 per CU) runs the 4-wave kernel, kt_prefill (2 tiles) the key-split kernel."""
     wl = make(name)
     print(f"[gpu-test] pure prefill graph {name}", flush=True)
     t = wl.tensors(device="cuda")
@@ -582,6 +583,8 @@ def test_pure_prefill_graph_replay(gpu, name):
     L = lib()
     meta = wl.meta(L.hip_attn_prefill_tile())
     assert not meta.decode and meta.single_rows() == 0 and wl.nq // wl.nkv == 2
+    want = {"c3": 4, "kt_prefill": 2}[name]  # LLMGEN_PREFILL_W4, LLMGEN_PREFILL_KEYSPLIT
+    assert L.hip_attn_prefill_plan(meta.n_tiles, wl.nq, wl.nkv, wl.hd, wl.block_size, 0) == want
     ws = wl.workspace()
     mgr = A.PagedAttentionManager()
     mgr.layers[0] = A.LayerState(t["kc"].clone(), t["vc"].clone())

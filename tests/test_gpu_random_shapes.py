@@ -13,6 +13,7 @@ import numpy as np
 import pytest
 
 from harness import assert_cache_equal, compare, run_gpu, run_oracle
+from llmgen_amd._lib import lib
 from llmgen_amd.step import Entry
 from llmgen_amd.workloads import Workload, _tables, to_u16
 
@@ -79,7 +80,9 @@ def _random_prefill_workload(case: int) -> Workload:
 def test_random_gqa2_prefill_matches_oracle(gpu, case):
     wl = _random_prefill_workload(case)
     print(f"[gpu-test] {wl.name}: {wl.note}", flush=True)
-    assert wl.meta(64).single_rows() == 0  # a pure prefill step: the key-split kernel runs
+    m = wl.meta(64)
+    assert m.single_rows() == 0  # a pure prefill step: the key-split kernel runs (small steps)
+    assert lib().hip_attn_prefill_plan(m.n_tiles, wl.nq, wl.nkv, wl.hd, wl.block_size, 0) == 2
     t = wl.tensors(device="cuda")
     out, kc, vc = run_gpu(wl, t)
     okc, ovc, _, of = run_oracle(wl, t, threads=16)
