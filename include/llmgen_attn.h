@@ -118,6 +118,7 @@ enum {
     LLMGEN_PREFILL_W2 = 3,        /* 2-wave workgroups, one head (G = 1) */
     LLMGEN_PREFILL_W4 = 4,        /* 4-wave workgroups, two heads */
     LLMGEN_PREFILL_W8 = 5,        /* 8-wave workgroups, four heads */
+    LLMGEN_PREFILL_SPLIT = 6,     /* 4-wave workgroups, the heaviest tiles' units split over two workgroups */
     LLMGEN_PREFILL_ROWS_LAUNCH = 16
 };
 int hip_attn_prefill_plan(int n_tiles, int nq, int nkv, int hd, int block_size, int single_rows);
@@ -132,14 +133,19 @@ int hip_attn_prefill_tile(void);
  *   LLMGEN_OPT_DECODE_ROW_WAVES    4 (default) or 8 waves per workgroup for the decode rows of a prefill step;
  *   LLMGEN_OPT_DECODE_MERGE_KERNEL 1: merge split-K partials in a separate merge kernel (the path of launches with
  *                                  more than 2^18 (sequence, kv head) pairs), 0 (default): in the decode kernel.
- * Defaults are read from the environment (SV_ATTN_PART, LLMGEN_DECODE_ROW_WAVES, LLMGEN_DECODE_MERGE) on first
- * use.  Returns the previous value, or -1 (and prints one line) for an unknown option or a bad value.  Not
+ *   LLMGEN_OPT_PREFILL_SPLIT_TILES -1 (default): the launcher's own count of heavy tiles whose units a pure
+ *                                  prefill step at G = 2 splits over two workgroups (LLMGEN_PREFILL_SPLIT);
+ *                                  0: no split; n > 0: the n heaviest tiles (at most what the scratch holds).
+ * Defaults are read from the environment (SV_ATTN_PART, LLMGEN_DECODE_ROW_WAVES, LLMGEN_DECODE_MERGE,
+ * LLMGEN_PREFILL_SPLIT_TILES) on first use.  Returns the previous value, or -1 (and prints one line) for an unknown
+ * option or a bad value (for LLMGEN_OPT_PREFILL_SPLIT_TILES, -1 is also its automatic setting).  Not
  * thread-safe; set options between launches. */
 enum {
     LLMGEN_OPT_ATTN_PART_MIN = 0,
     LLMGEN_OPT_DECODE_ROW_WAVES = 1,
     LLMGEN_OPT_DECODE_MERGE_KERNEL = 2,
-    LLMGEN_OPT_COUNT = 3
+    LLMGEN_OPT_PREFILL_SPLIT_TILES = 3,
+    LLMGEN_OPT_COUNT = 4
 };
 int hip_attn_set_option(int option, int value);
 

@@ -73,6 +73,7 @@ static void load_opts() {
                 g_opts[LLMGEN_OPT_ATTN_PART_MIN]);
     g_opts[LLMGEN_OPT_DECODE_ROW_WAVES] = env("LLMGEN_DECODE_ROW_WAVES", 4);
     g_opts[LLMGEN_OPT_DECODE_MERGE_KERNEL] = env("LLMGEN_DECODE_MERGE", 0);
+    g_opts[LLMGEN_OPT_PREFILL_SPLIT_TILES] = env("LLMGEN_PREFILL_SPLIT_TILES", -1);
     g_opts_loaded = true;
 }
 
@@ -104,7 +105,7 @@ int hip_attn_set_option(int option, int value) {
         fprintf(stderr, "[llmgen-hip] hip_attn_set_option: decode-row waves must be 4 or 8 (got %d)\n", value);
         return -1;
     }
-    if (value < 0) {
+    if (value < 0 && !(option == LLMGEN_OPT_PREFILL_SPLIT_TILES && value == -1)) {
         fprintf(stderr, "[llmgen-hip] hip_attn_set_option: negative value %d\n", value);
         return -1;
     }

@@ -40,6 +40,8 @@
 
 #include <math.h>
 
+#include <algorithm>
+#include <stdlib.h>
 #include <type_traits>
 
 namespace {
@@ -81,6 +83,145 @@ void launch_prefill(int mode, int head_groups, bf16_t *out, const bf16_t *q, con
     if (mode == DMA_BLOCK) go(std::integral_constant<int, DMA_BLOCK>{});
     else if (mode == DMA_ROW4) go(std::integral_constant<int, DMA_ROW4>{});
     else go(std::integral_constant<int, DMA_FLAT>{});
+}
+
+// ---- pure prefill with the heaviest units split over two workgroups ----
+//
+// A pure prefill step at G = 2 too large for the key-split kernel is as long as its heaviest unit: the last tiles
+// of a long prompt need every key tile before them, one after another (c3: 56 key tiles).  Here the units of the
+// n_heavy heaviest tiles (the end of the executor's lightest-first list) each get two 4-wave workgroups, one per
+// half of the unit's key tiles; both leave their partial (O, m, l) in the library's scratch array and the one that
+// finishes second merges the two in a fixed order (piece 0, then piece 1: bit-reproducible) and stores the rows.
+// Every other unit is one workgroup as in the 4-wave kernel.  The grid keeps the KV head fastest, so a KV head
+// stays on its XCD.
+constexpr int SPLIT_MAX_UNITS = 256;  // heavy units (tile x KV head x head group) one launch can split
+__device__ __align__(256) float g_split_part[(size_t)SPLIT_MAX_UNITS * 2 * PART_FLOATS];
+__device__ int g_split_counters[SPLIT_MAX_UNITS];
+
+template <int MODE>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+    attn_prefill_split_kernel(bf16_t *__restrict__ out, const bf16_t *__restrict__ q, const bf16_t *__restrict__ kc,
+                              const bf16_t *__restrict__ vc, const int *__restrict__ block_tables,
+                              const int *__restrict__ ctx_lens, const int *__restrict__ cu_q,
+                              const int *__restrict__ tile_seq, const int *__restrict__ tile_q0, int n_tiles, int nq,
+                              int nkv, int G, int head_groups, int max_blocks, int block_size, int bs_shift,
+                              float scale_log2, int n_heavy, float *__restrict__ part, int *__restrict__ counters) {
+    __shared__ __attribute__((aligned(16))) unsigned char lds[sizeof(PrefillLds<4, 1>)];
+    __shared__ int s_last;
+    const int Q = nkv * head_groups;  // units per tile
+    const long b = blockIdx.x;
+    auto body = [&](int bid, int j0, int j1, float *dst) {
+        prefill_body<4, MODE, 1, true>(out, q, kc, vc, block_tables, ctx_lens, cu_q, tile_seq, tile_q0, n_tiles, nq,
+                                      nkv, G, head_groups, max_blocks, block_size, bs_shift, scale_log2, bid, lds, j0,
+                                      j1, dst);
+    };
+    // Grid order, longest first over all pieces: the halves of heavy tile k (2 groups of Q workgroups), then the
+    // unsplit tile n_heavy + k, whose units are about as long as those halves, for k < periods; then what is left
+    // of either kind.  t = the tile's position from the end of the list; half = -1 for an unsplit unit.
+    const int n_light = n_tiles - n_heavy, periods = min(n_heavy, n_light);
+    const long g = b / Q;
+    const int within = (int)(b % Q);
+    int t, half;
+    if (g < 3L * periods) {
+        const int k = (int)(g / 3), r = (int)(g % 3);
+        t = r < 2 ? k : n_heavy + k;
+        half = r < 2 ? r : -1;
+    } else if (n_heavy > periods) {  // heavy tiles left over (fewer light tiles than heavy ones)
+        const long r = g - 3L * periods;
+        if (r < 2L * (n_heavy - periods)) {
+            t = periods + (int)(r / 2);
+            half = (int)(r % 2);
+        } else {
+            t = n_heavy + periods + (int)(r - 2L * (n_heavy - periods));
+            half = -1;
+        }
+    } else {
+        t = n_heavy + (int)(g - 2L * periods);  // light tiles from n_heavy + periods on
+        half = -1;
+    }
+    const int bid = t * Q + within;  // the unit, numbered as in the one-unit-per-workgroup grid
+    if (half < 0) {  // one workgroup, all its key tiles
+        body(bid, 0, -1, nullptr);
+        return;
+    }
+    const int tile = n_tiles - 1 - t;
+    const int s = tile_seq[tile], q_len = cu_q[s + 1] - cu_q[s], ctx = ctx_lens[s];
+    const int n = q_len > 1 && ctx >= q_len ? (ctx - q_len + min(tile_q0[tile] + BQ, q_len) + BK - 1) / BK : 0;
+    if (n < 2) {  // nothing to split (a one-tile unit, a padding or single-row segment): the first half runs it
+        if (half == 0) body(bid, 0, -1, nullptr);
+        return;
+    }
+    float *mine = part + ((long)bid * 2 + half) * PART_FLOATS;
+    body(bid, half ? n / 2 : 0, half ? -1 : n / 2, mine);
+    // publish, then draw a ticket: the second half to arrive merges (the partials are device-coherent stores,
+    // complete before the barrier; the merger reads them with device-coherent loads after an acquire fence)
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0)
+        s_last = __hip_atomic_fetch_add(counters + bid, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 1;
+    __syncthreads();
+    if (!s_last) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    const float *const pieces[2] = {part + (long)bid * 2 * PART_FLOATS, part + ((long)bid * 2 + 1) * PART_FLOATS};
+    prefill_merge_store<2>(out, cu_q, tile_seq, tile_q0, n_tiles, nq, nkv, G, head_groups, bid, pieces);
+    if (threadIdx.x == 0) __hip_atomic_store(counters + bid, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <typename T>
+T *symbol_address(const T &sym) {
+    static T *ptr[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    if (!ptr[dev]) {
+        void *p = nullptr;
+        if (hipGetSymbolAddress(&p, sym) != hipSuccess) return nullptr;
+        ptr[dev] = (T *)p;
+    }
+    return ptr[dev];
+}
+
+// Heavy tiles to split for a pure prefill step of two-head units (0 = do not split).  Automatic: half a CU's worth
+// of units, n_heavy * nkv * head_groups = CUs / 2, on steps of at most 5 units per CU; steps with more are bound by
+// throughput, not by their heaviest units.  Measured on c3 (99 tiles x 8 KV heads), interleaved grid, same box:
+// 0 tiles 78.7 us, 6: 74.2, 10: 71.9, 14: 67.3, 16: 66.8, 20: 68.5, 22: 78.4 (the unsplit tiles beside the halves
+// then outlast them), 32: 78.6 us; two other draws of c3's prompt lengths 79.7 -> 70.5 and 79.0 -> 68.7 us at 16;
+// single prompts of 5632 / 8192 tokens 137.9 -> 139.0 / 272.3 -> 267.0 us, 16384 tokens (8 units per CU, so not
+// split) 985.9 against 995.1 us when split.  LLMGEN_OPT_PREFILL_SPLIT_TILES overrides the count (0 = off).
+int split_heavy_tiles(int n_tiles, int nkv, int head_groups) {
+    const int Q = nkv * head_groups;
+    const int opt = llmgen_opt(LLMGEN_OPT_PREFILL_SPLIT_TILES);
+    int h;
+    if (opt >= 0) {
+        h = opt;
+    } else {
+        const int cus = llmgen_num_cus();
+        if ((long)n_tiles * Q > 5L * cus) return 0;
+        h = std::max(1, cus / (2 * Q));
+    }
+    h = std::min(h, n_tiles);
+    h = std::min(h, SPLIT_MAX_UNITS / Q);
+    return h > 0 ? h : 0;
+}
+
+bool launch_prefill_split(int mode, bf16_t *out, const bf16_t *q, const bf16_t *kc, const bf16_t *vc, const int *bt,
+                          const int *ctx, const int *cu_q, const int *tile_seq, const int *tile_q0, int n_tiles,
+                          int nq, int nkv, int G, int max_blocks, int block_size, int bs_shift, float sl2) {
+    const int head_groups = G / 2;
+    const int h = split_heavy_tiles(n_tiles, nkv, head_groups);
+    if (h <= 0) return false;
+    float *part = reinterpret_cast<float *>(symbol_address(HIP_SYMBOL(g_split_part)));
+    int *counters = reinterpret_cast<int *>(symbol_address(HIP_SYMBOL(g_split_counters)));
+    if (!part || !counters) return false;
+    const long grid = ((long)n_tiles + h) * nkv * head_groups;
+    auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(256), 0, g_llmgen_stream, out, q, kc, vc, bt, ctx, cu_q,
+                           tile_seq, tile_q0, n_tiles, nq, nkv, G, head_groups, max_blocks, block_size, bs_shift,
+                           sl2, h, part, counters);
+    };
+    if (mode == DMA_BLOCK) go(attn_prefill_split_kernel<DMA_BLOCK>);
+    else if (mode == DMA_ROW4) go(attn_prefill_split_kernel<DMA_ROW4>);
+    else go(attn_prefill_split_kernel<DMA_FLAT>);
+    return true;
 }
 
 }  // namespace
@@ -126,7 +267,9 @@ PrefillPlan plan_prefill(int n_tiles, int G, int nkv, int single_rows) {
         // 1069 us).  With decode rows beside it a 128 KB workgroup finds no room next to the decode kernel's waves.
         p.kernel = single_rows == 0 && (long)n_tiles * nkv * head_groups * 2 <= 5L * llmgen_num_cus()
                        ? LLMGEN_PREFILL_KEYSPLIT
-                       : LLMGEN_PREFILL_W4;
+                       : (single_rows == 0 && G == 2 && split_heavy_tiles(n_tiles, nkv, head_groups) > 0
+                              ? LLMGEN_PREFILL_SPLIT
+                              : LLMGEN_PREFILL_W4);
     } else {
         p.kernel = LLMGEN_PREFILL_W8;
     }
@@ -178,7 +321,14 @@ extern "C" void hip_attn_prefill_rows(bf16_t *out, const bf16_t *q, const bf16_t
         llmgen_decode_rows_of_prefill(out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq, n_tiles, nq,
                                       nkv, max_blocks, block_size, scale, side);
     }
-    switch (plan.kernel) {
+    PrefillPlan run = plan;
+    if (plan.kernel == LLMGEN_PREFILL_SPLIT &&
+        !launch_prefill_split(mode, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq, tile_q0,
+                              n_tiles, nq, nkv, G, max_blocks, block_size, bs_shift, sl2))
+        run.kernel = LLMGEN_PREFILL_W4;
+    switch (run.kernel) {
+        case LLMGEN_PREFILL_SPLIT:
+            break;
         case LLMGEN_PREFILL_W2:
             launch_prefill<2>(mode, head_groups, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq,
                               tile_q0, n_tiles, nq, nkv, G, max_blocks, block_size, bs_shift, sl2);

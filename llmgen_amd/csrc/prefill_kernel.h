@@ -62,15 +62,25 @@ struct PrefillLds {
     __attribute__((aligned(16))) bf16_t V1[ONE_STAGE ? 8 : KS * TILE];
 };
 
+// Split-K partial result of one unit (4 waves x 64 lanes): per wave, the unnormalised O^T accumulator values
+// [64][lane], then m [lane] and l [lane] (before the half-wave sum).
+constexpr int PART_WAVE_FLOATS = 66 * 64;
+constexpr int PART_FLOATS = 4 * PART_WAVE_FLOATS;
+
 // The prefill workgroup's work, as a device function so that other kernels can run it as one of their workgroup
-// roles: bid plays the part of the 1-D grid position, lds holds a PrefillLds<NW, KS>.
-template <int NW, int MODE, int KS>
+// roles: bid plays the part of the 1-D grid position, lds holds a PrefillLds<NW, KS>.  With SK (one key group,
+// four waves) the workgroup runs only key tiles [j0, j1) of the unit (j1 < 0: to the unit's last tile); if part
+// is not null it leaves the unit's partial result there (device-coherent stores, PART_FLOATS floats) instead of
+// storing rows.
+template <int NW, int MODE, int KS, bool SK = false>
 __device__ __forceinline__ void prefill_body(bf16_t *__restrict__ out, const bf16_t *__restrict__ q, const bf16_t *__restrict__ kc,
                         const bf16_t *__restrict__ vc, const int *__restrict__ block_tables,
                         const int *__restrict__ ctx_lens, const int *__restrict__ cu_q,
                         const int *__restrict__ tile_seq, const int *__restrict__ tile_q0, int n_tiles, int nq,
                         int nkv, int G, int head_groups, int max_blocks, int block_size, int bs_shift,
-                        float scale_log2, int bid, unsigned char *lds) {
+                        float scale_log2, int bid, unsigned char *lds, int j0 = 0, int j1 = 0,
+                        float *__restrict__ part = nullptr) {
+    static_assert(!SK || (KS == 1 && NW == 4), "key ranges are for 4-wave, one-group workgroups");
     constexpr int NWG = NW / KS;     // waves per key group
     constexpr int LOADS = 16 / NWG;  // 4-row DMA instructions per wave per tile, for K and for V each
 
@@ -116,8 +126,10 @@ __device__ __forceinline__ void prefill_body(bf16_t *__restrict__ out, const bf1
     const long head_off = (long)kvh * block_size * HD;
     const int base_pos = ctx - q_len;                // position of segment row 0
     const int kend = base_pos + min(q0 + BQ, q_len);  // keys needed by the whole tile
-    const int n_iter = (kend + BK - 1) / BK;  // key tiles
-    const int n_super = (n_iter + KS - 1) / KS;  // iterations: one tile per key group each
+    const int n_all = (kend + BK - 1) / BK;  // key tiles of the unit
+    const int n_iter = SK && j1 >= 0 ? min(j1, n_all) : n_all;  // SK: the end of this workgroup's key range
+    const int it_base = SK ? j0 : 0;                             // first key tile
+    const int n_super = SK ? n_iter - j0 : (n_iter + KS - 1) / KS;  // iterations: one tile per key group each
 
     // ---- Q fragments (B operand): lane holds row r0+l32, dims c*16 + hh*8 .. +8 ----
     const int my_row = r0 + l32;
@@ -140,7 +152,7 @@ __device__ __forceinline__ void prefill_body(bf16_t *__restrict__ out, const bf1
     //      that swizzles onto it ----
     const int drow = lane >> 4, dchunk = lane & 15;
     auto issue = [&](int it, bf16_t *Kd, bf16_t *Vd) {
-        const int ti = it * KS + kg;
+        const int ti = it_base + it * KS + kg;
         if (KS > 1 && ti >= n_iter) return;  // the unit's last iteration has no tile for this group
         Kd += kg * TILE;
         Vd += kg * TILE;
@@ -320,7 +332,7 @@ __device__ __forceinline__ void prefill_body(bf16_t *__restrict__ out, const bf1
         }
     };
     auto compute = [&](int it, const bf16_t *Ks, const bf16_t *Vs) {
-        const int ti = it * KS + kg;
+        const int ti = it_base + it * KS + kg;
         const int kb0 = ti * BK;
         Ks += kg * TILE;
         Vs += kg * TILE;
@@ -387,6 +399,20 @@ __device__ __forceinline__ void prefill_body(bf16_t *__restrict__ out, const bf1
             for (int r = 0; r < 16; ++r) o[db][r] = o[db][r] * c0 + xo[(db * 16 + r) * 64 + lane] * c1;
     }
 
+    if constexpr (SK) {
+        if (part) {  // leave the partial result (the merging workgroup reads it with device-coherent loads)
+            if (!wave_active) return;
+            float *pw = part + wave * PART_WAVE_FLOATS + lane;
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    __hip_atomic_store(pw + (db * 16 + r) * 64, o[db][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(pw + 64 * 64, m_run, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(pw + 65 * 64, l_run, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return;
+        }
+    }
     // ---- normalise and store: lane holds dims db*32 + (r/4)*8 + hh*4 + r%4 of row my_row ----
     if (!wave_active) return;
     const float l_tot = l_run + lane_xor(l_run, 32);
@@ -400,6 +426,55 @@ __device__ __forceinline__ void prefill_body(bf16_t *__restrict__ out, const bf1
             u32x2_t w;
             w[0] = pack_bf16x2(o[db][rr * 4 + 0] * inv, o[db][rr * 4 + 1] * inv);
             w[1] = pack_bf16x2(o[db][rr * 4 + 2] * inv, o[db][rr * 4 + 3] * inv);
+            *reinterpret_cast<u32x2_t *>(orow + db * 32 + rr * 8) = w;
+        }
+}
+
+// Merge the partial results of one unit (4-wave, one-group layout of prefill_body<4, *, 1, true>): the
+// log-sum-exp combination of its key-range pieces in the order given, lane by lane (each lane holds the same row
+// and dims in every piece), then the normalisation and bf16 store of prefill_body.  Device-coherent loads: the
+// pieces were written by other workgroups.
+template <int NP>
+__device__ __forceinline__ void prefill_merge_store(bf16_t *__restrict__ out, const int *__restrict__ cu_q,
+                                                    const int *__restrict__ tile_seq, const int *__restrict__ tile_q0,
+                                                    int n_tiles, int nq, int nkv, int G, int head_groups, int bid,
+                                                    const float *const (&pieces)[NP]) {
+    const int kvh = bid % nkv, rest = bid / nkv, hg = rest % head_groups;
+    const int tile = n_tiles - 1 - rest / head_groups;
+    const int s = tile_seq[tile], q0 = tile_q0[tile];
+    const int q_beg = cu_q[s], q_len = cu_q[s + 1] - q_beg;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int head = kvh * G + hg * 2 + (wave >> 1);
+    const int r0 = q0 + (wave & 1) * 32, l32 = lane & 31, hh = lane >> 5;
+    if (r0 >= q_len) return;  // an inactive wave left no partial
+    auto ld = [&](const float *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+    float M = -INFINITY;
+#pragma unroll
+    for (int p = 0; p < NP; ++p) M = fmaxf(M, ld(pieces[p] + wave * PART_WAVE_FLOATS + 64 * 64 + lane));
+    const float Mu = M == -INFINITY ? 0.f : M;
+    float o[64], l = 0.f;
+#pragma unroll
+    for (int v = 0; v < 64; ++v) o[v] = 0.f;
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        const float *pw = pieces[p] + wave * PART_WAVE_FLOATS + lane;
+        const float c = fast_exp2(ld(pw + 64 * 64) - Mu);
+        l += ld(pw + 65 * 64) * c;
+#pragma unroll
+        for (int v = 0; v < 64; ++v) o[v] += ld(pw + v * 64) * c;
+    }
+    const float l_tot = l + lane_xor(l, 32);
+    const int my_row = r0 + l32;
+    if (my_row >= q_len) return;
+    const float inv = 1.f / l_tot;
+    bf16_t *orow = out + ((long)(q_beg + my_row) * nq + head) * HD + hh * 4;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            u32x2_t w;
+            w[0] = pack_bf16x2(o[db * 16 + rr * 4 + 0] * inv, o[db * 16 + rr * 4 + 1] * inv);
+            w[1] = pack_bf16x2(o[db * 16 + rr * 4 + 2] * inv, o[db * 16 + rr * 4 + 3] * inv);
             *reinterpret_cast<u32x2_t *>(orow + db * 32 + rr * 8) = w;
         }
 }

@@ -395,7 +395,8 @@ def test_prefill_plan_names_the_kernel_each_config_runs(gpu):
     """hip_attn_prefill_plan reports the launch hip_attn_prefill_rows makes, from the same rule: mixed steps at
     GQA 2 / 4 with a known single-row count run one mixed-step launch, c3 (99 tiles x 8 KV heads = 792 units of two
     heads, above 2.5 per CU) the 4-wave kernel, c5p (GQA 4, 256 tiles) the 8-wave four-head kernel, the small
-    pure prefills the key-split kernel, and an unknown count adds the separate decode-row launch."""
+    pure prefills the key-split kernel, and an unknown count adds the separate decode-row launch; c3 (792 two-head
+    units, 3.1 per CU) splits its heaviest tiles' units over two workgroups each."""
     L = lib()
     pf = L.hip_attn_prefill_tile()
     plan = {}
@@ -404,8 +405,8 @@ def test_prefill_plan_names_the_kernel_each_config_runs(gpu):
         m = wl.meta(pf)
         plan[name] = (L.hip_attn_prefill_plan(m.n_tiles, wl.nq, wl.nkv, wl.hd, wl.block_size, m.single_rows()),
                       L.hip_attn_prefill_plan(m.n_tiles, wl.nq, wl.nkv, wl.hd, wl.block_size, -1))
-    MIXED, KEYSPLIT, W2, W4, W8, ROWS = 1, 2, 3, 4, 5, 16
-    assert plan["c3"] == (W4, W4 | ROWS)
+    MIXED, KEYSPLIT, W2, W4, W8, SPLIT, ROWS = 1, 2, 3, 4, 5, 6, 16
+    assert plan["c3"] == (SPLIT, W4 | ROWS)
     assert plan["c4"] == (MIXED, W4 | ROWS)
     assert plan["c5p"] == (W8, W8 | ROWS)
     assert plan["kt_prefill"] == (KEYSPLIT, W4 | ROWS)
@@ -575,7 +576,9 @@ def test_mixed_step_graph_replay(gpu, name):
 def test_pure_prefill_graph_replay(gpu, name):
     """A pure prefill step at GQA 2 (no decode-row launch) captured into a graph: three replays with eager torch
     work between them each give the eager step's output bit for bit.  c3 (792 two-head units, above the key-split
-    rule's 2.5 per CU) runs the 4-wave kernel, kt_prefill (2 tiles) the key-split kernel."""
+    rule's 2.5 per CU) runs the 4-wave kernel with its heaviest units split over two workgroups (halves merged
+    through the library's scratch, their ticket counters back at 0 after every launch), kt_prefill (2 tiles) the
+    key-split kernel."""
     wl = make(name)
     print(f"[gpu-test] pure prefill graph {name}", flush=True)
     t = wl.tensors(device="cuda")
@@ -583,7 +586,7 @@ def test_pure_prefill_graph_replay(gpu, name):
     L = lib()
     meta = wl.meta(L.hip_attn_prefill_tile())
     assert not meta.decode and meta.single_rows() == 0 and wl.nq // wl.nkv == 2
-    want = {"c3": 4, "kt_prefill": 2}[name]  # LLMGEN_PREFILL_W4, LLMGEN_PREFILL_KEYSPLIT
+    want = {"c3": 6, "kt_prefill": 2}[name]  # LLMGEN_PREFILL_SPLIT, LLMGEN_PREFILL_KEYSPLIT
     assert L.hip_attn_prefill_plan(meta.n_tiles, wl.nq, wl.nkv, wl.hd, wl.block_size, 0) == want
     ws = wl.workspace()
     mgr = A.PagedAttentionManager()
