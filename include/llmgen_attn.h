@@ -99,7 +99,10 @@ void hip_attn_prefill(uint16_t *out, const uint16_t *q, const uint16_t *k_cache,
  * unwritten (pass -1 when unsure).  With a count > 0 at G = 2 or 4 the whole step is one launch in which workgroups
  * take either a prefill unit or a decode row; it is fastest when the list holds the single-row tiles first (as
  * llmgen_fill_meta orders it) and gives the same result for any order.  For GQA >= 2 a count of 0 also selects,
- * on steps of at most 2.5 (query tile, KV head, head pair) units per CU, the key-split prefill kernel.  Which
+ * on steps of at most 2.5 (query tile, KV head, head pair) units per CU, the key-split prefill kernel, and at
+ * GQA 2 on steps of up to 5 units per CU the heavy-tile split kernel, whose split units keep their partials in a
+ * library-owned device array (two such launches running at once on different streams of one GPU race on it;
+ * launches on one stream and graph replays are safe).  Which
  * kernel runs (hip_attn_prefill_plan) changes the summation order, so the same rows computed in steps of different
  * composition or with a different count can differ in their last bits (same tolerance); one call is always
  * bit-reproducible. */
