@@ -188,10 +188,10 @@ DECISIVE = 4.0  # a row-step is decisive when its top-2 margin exceeds this many
 
 
 def _record(name: str, lines) -> None:
-    """Keep a run's greedy-id evidence: written to <repo>/gpurun_out/<name> when that folder exists (a GPU box
-    run returns it), so the ids, margins and agreement counts survive ``pytest -q``."""
-    out_dir = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "gpurun_out")
-    if os.path.isdir(out_dir):
+    """Keep a run's greedy-id evidence: written to $LLMGEN_RECORD_DIR/<name> when that variable names a folder, so
+    the ids, margins and agreement counts survive ``pytest -q``."""
+    out_dir = os.environ.get("LLMGEN_RECORD_DIR", "")
+    if out_dir and os.path.isdir(out_dir):
         with open(os.path.join(out_dir, name), "w") as f:
             f.write("\n".join(lines) + "\n")
 

@@ -151,8 +151,8 @@ pub fn maxParts(s: usize, max_model_len: usize) usize {
     return (max_model_len + ps - 1) / ps;
 }
 
-/// The step's count of single-row segments, if the engine's StepState carries it (the `single_rows: c_int = -1`
-/// field that INTEGRATION.md adds to common.zig, set by bindStep from step_hints.singleRows), else -1.
+/// The step's count of single-row segments, if the engine's StepState carries it (a `single_rows: c_int = -1`
+/// field added to common.zig's StepState, set by bindStep from step_hints.singleRows), else -1.
 fn singleRowsOf(st: anytype) c_int {
     if (@hasField(@TypeOf(st.*), "single_rows")) return st.single_rows;
     return -1;
