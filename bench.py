@@ -147,7 +147,18 @@ def bench_extra(name: str, iters: int) -> dict:
         tf = wl.attention_flops() / (ms * 1e-3) / 1e12
         gbs = wl.decode_bytes() / (ms * 1e-3) / 1e9
         r.update(prefill_TFLOPs=round(tf, 1), mfma_frac=round(tf / BF16_PEAK_TFLOPS, 4), kv_GBs=round(gbs, 1))
+        # which kernel the launcher ran for this step (the launcher's own record, hip_attn_prefill_plan)
+        plan = st.L.hip_attn_prefill_plan(st.g.n_tiles, wl.nq, wl.nkv, wl.hd, wl.block_size, st.g.single_rows)
+        r["kernel"] = PREFILL_KERNELS.get(plan & 15, f"plan {plan}") + (
+            " + decode rows on the side stream" if plan >= 0 and plan & 16 else "")
     return r
+
+
+PREFILL_KERNELS = {1: "attn_mixed_kernel (prefill units and decode rows as workgroup roles)",
+                   2: "attn_prefill_kernel<8, *, 2> (key split in the workgroup)",
+                   3: "attn_prefill_kernel<2, *, 1>", 4: "attn_prefill_kernel<4, *, 1>",
+                   5: "attn_prefill_kernel<8, *, 1>",
+                   6: "attn_prefill_split_kernel (heaviest tiles' units over two workgroups)"}
 
 
 def bench_qk_fused(name: str, iters: int) -> dict:
