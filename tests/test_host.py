@@ -197,3 +197,18 @@ def test_workload_slots_are_unique():
         m = make(name).meta(64)
         s = m.slots[m.slots >= 0]
         assert len(np.unique(s)) == len(s), name
+
+
+def test_bench_kernel_names_follow_the_header():
+    """bench.py names the prefill kernel of each config from hip_attn_prefill_plan's value; its table must cover
+    exactly the LLMGEN_PREFILL_* kernel values that include/llmgen_attn.h declares."""
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    hdr = open(os.path.join(root, "include", "llmgen_attn.h")).read()
+    vals = {int(v) for name, v in re.findall(r"LLMGEN_PREFILL_(\w+)\s*=\s*(\d+)", hdr) if name != "ROWS_LAUNCH"}
+    assert vals == {1, 2, 3, 4, 5, 6}
+    sys.path.insert(0, root)
+    import bench
+
+    assert set(bench.PREFILL_KERNELS) == vals
+    assert "split" in bench.PREFILL_KERNELS[int(re.search(r"LLMGEN_PREFILL_SPLIT\s*=\s*(\d+)", hdr).group(1))]
+    assert "mixed" in bench.PREFILL_KERNELS[int(re.search(r"LLMGEN_PREFILL_MIXED\s*=\s*(\d+)", hdr).group(1))]
