@@ -5,6 +5,8 @@
 
 #include <math.h>
 
+#include <type_traits>
+
 namespace llmgen_decode {
 
 // K and V rows are read once, whole (four full 256-byte rows per instruction): nontemporal loads keep them from
@@ -144,17 +146,28 @@ __device__ __forceinline__ void decode_split_body(bf16_t *__restrict__ out, floa
 #pragma unroll
     for (int db = 0; db < 8; ++db) o4[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    // K and V: token rgrp + 4j, dims col*8 (four whole 256-byte rows per load instruction).
+    // K rows go straight from HBM into this wave's LDS slice (LDS DMA, no registers); V rows into registers,
+    // token rgrp + 4j, dims col*8 (four whole 256-byte rows per load instruction).
     struct Buf {
-        u32x4_t kr[4 * NT];
+        u32x4_t knew;  // the fused token's K row chunk (FUSE only)
         u32x4_t vf[4 * NT];
     };
-    auto load = [&](int r, Buf &b) {
+    bf16_t *k_lds_flat = reinterpret_cast<bf16_t *>(&k_lds[0][0][0]);
+    int kb0_blk = 0;
+    __amdgpu_buffer_rsrc_t krs0, krs1;
+    int vt_keep[4 * NT];  // this round's (clamped) token of load j, for the fused-token fix-up
+    // SCAL: the wave's rows lie in at most two blocks of a power-of-two size: scalar block-table reads and K rows
+    // through one buffer descriptor per block.  The round loop is instantiated once per case.
+    auto load = [&](int r, Buf &b, auto scal) {
+        constexpr bool SCAL = decltype(scal)::value;
         const int wbase = r * RTOK + wave * WTOK;
         int vt[4 * NT], vblk[4 * NT];
 #pragma unroll
         for (int j = 0; j < 4 * NT; ++j) vt[j] = t0 + min(wbase + rgrp + 4 * j, n - 1);
-        if (POW2 && block_size >= WTOK) {
+#pragma unroll
+        for (int j = 0; j < 4 * NT; ++j) vt_keep[j] = vt[j];
+        if (fuse) b.knew = ld16(k_new + new_row + col * 8);  // issued before the K rows: covered by their wait
+        if (SCAL) {
             // the wave's WTOK tokens touch at most two blocks: two scalar block-table reads (scalar cache,
             // their own wait counter), then a per-lane select
             const int b0 = __builtin_amdgcn_readfirstlane((t0 + min(wbase, n - 1)) >> bs_shift);
@@ -162,18 +175,47 @@ __device__ __forceinline__ void decode_split_body(bf16_t *__restrict__ out, floa
             const int p0 = bt[b0], p1 = bt[b1];
 #pragma unroll
             for (int j = 0; j < 4 * NT; ++j) vblk[j] = (vt[j] >> bs_shift) == b0 ? p0 : p1;
+            kb0_blk = b0;
+            krs0 = __builtin_amdgcn_make_buffer_rsrc((void *)(kbase + (long)p0 * blk_stride), (short)0,
+                                                     block_size * HD * 2, 0x00020000);
+            krs1 = __builtin_amdgcn_make_buffer_rsrc((void *)(kbase + (long)p1 * blk_stride), (short)0,
+                                                     block_size * HD * 2, 0x00020000);
         } else {
             // all block-table reads first (independent), then all K/V reads
 #pragma unroll
             for (int j = 0; j < 4 * NT; ++j) vblk[j] = bt[blk_index<POW2>(vt[j], block_size, bs_shift)];
         }
+        // K: instruction j fills rows 4j..4j+3 of the slice (1 KB); lane l writes physical chunk l % 16 of row
+        // 4j + l / 16, so it reads the logical chunk that the XOR swizzle puts there.  The four rows of an
+        // instruction share a block (block sizes are multiples of 4 on this path), whose descriptor is picked per
+        // instruction; other block sizes take per-lane addresses.  Nontemporal, as the V rows.
+        if (SCAL) {
+            const int wb = __builtin_amdgcn_readfirstlane(wbase);
 #pragma unroll
-        for (int j = 0; j < 4 * NT; ++j) {
-            const int off = vt[j] - blk_index<POW2>(vt[j], block_size, bs_shift) * block_size;
-            const long row = (long)vblk[j] * blk_stride + (long)off * HD + col * 8;
-            const bool mine = fuse && vt[j] == ctx - 1;
-            b.kr[j] = ld16_stream(mine ? k_new + new_row + col * 8 : kbase + row);
+            for (int j = 0; j < 4 * NT; ++j) {
+                const int kch = col ^ ((rgrp + 4 * j) & 15);
+                const int u = t0 + min(wb + 4 * j, n - 1);  // the instruction's first row (wave-uniform)
+                const int voff = ((vt[j] & (block_size - 1)) * HD + kch * 8) * 2;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    (u >> bs_shift) == kb0_blk ? krs0 : krs1,
+                    (__attribute__((address_space(3))) void *)&k_lds_flat[(wave * WTOK + 4 * j) * HD], 16, voff, 0,
+                    0, LLMGEN_CPOL_NT);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4 * NT; ++j) {
+                const int kch = col ^ ((rgrp + 4 * j) & 15);
+                const int off = vt[j] - blk_index<POW2>(vt[j], block_size, bs_shift) * block_size;
+                const long row = (long)vblk[j] * blk_stride + (long)off * HD + kch * 8;
+                __builtin_amdgcn_global_load_lds(
+                    (const __attribute__((address_space(1))) void *)(kbase + row),
+                    (__attribute__((address_space(3))) void *)&k_lds_flat[(wave * WTOK + 4 * j) * HD], 16, 0,
+                    LLMGEN_CPOL_NT);
+            }
         }
+        // the V loads below must be issued after these: compute() waits for the K rows by counting the V loads
+        // still outstanding (vmcnt(4 NT)); the compiler does not order LDS-DMA writes against LDS reads itself
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int j = 0; j < 4 * NT; ++j) {
             const int off = vt[j] - blk_index<POW2>(vt[j], block_size, bs_shift) * block_size;
@@ -185,12 +227,16 @@ __device__ __forceinline__ void decode_split_body(bf16_t *__restrict__ out, floa
 
     auto compute = [&](int r, const Buf &b) {
         const int wbase = r * RTOK + wave * WTOK;
-        // ---- K rows into this wave's LDS slice, then the MFMA B fragments back out of it (tile tau, chunk c =
+        // ---- this wave's K rows in its LDS slice, then the MFMA B fragments out of it (tile tau, chunk c =
         //      dims c*32 + rgrp*8 of token tau*16 + col); the XOR swizzle keeps both directions conflict-free ----
+        // vmcnt(4 NT): the K rows (issued before the 4 NT V loads) have landed
+        __builtin_amdgcn_s_waitcnt(LLMGEN_WAIT_VMCNT(4 * NT));
+        if (fuse) {  // the step's own token: its row comes from k_new, not from the slot being written
 #pragma unroll
-        for (int j = 0; j < 4 * NT; ++j) {
-            const int tok = rgrp + 4 * j;
-            k_lds[wave][tok][col ^ (tok & 15)] = b.kr[j];
+            for (int j = 0; j < 4 * NT; ++j) {
+                const int tok = rgrp + 4 * j;
+                if (vt_keep[j] == ctx - 1) k_lds[wave][tok][col ^ (tok & 15)] = b.knew;
+            }
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -327,9 +373,16 @@ __device__ __forceinline__ void decode_split_body(bf16_t *__restrict__ out, floa
     };
 
     Buf buf;
-    for (int r = 0; r < rounds; ++r) {
-        load(r, buf);
-        compute(r, buf);
+    if (POW2 && block_size >= WTOK) {
+        for (int r = 0; r < rounds; ++r) {
+            load(r, buf, std::true_type{});
+            compute(r, buf);
+        }
+    } else {
+        for (int r = 0; r < rounds; ++r) {
+            load(r, buf, std::false_type{});
+            compute(r, buf);
+        }
     }
 
     // ---- per-wave totals ----

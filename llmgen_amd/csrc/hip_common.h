@@ -75,6 +75,12 @@ __device__ __forceinline__ float lane_xor(float x, int mask) {
     return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, __builtin_bit_cast(int, x)));
 }
 
+// s_waitcnt immediate that waits until at most n vector-memory operations of this wave are outstanding
+// (vmcnt, 6 bits split over [3:0] and [15:14]) and leaves the export and LDS counters unconstrained.
+#define LLMGEN_WAIT_VMCNT(n) (0x0f70 | ((n) & 15) | ((((n) >> 4) & 3) << 14))
+// cache-policy operand of the LDS-DMA builtins: nontemporal (the rows are read once)
+#define LLMGEN_CPOL_NT 2
+
 // 16-byte global load as four dwords.
 __device__ __forceinline__ u32x4_t ld16(const void *p) { return *reinterpret_cast<const u32x4_t *>(p); }
 

@@ -257,12 +257,15 @@ __device__ __forceinline__ void prefill_body(bf16_t *__restrict__ out, const bf1
         __builtin_amdgcn_sched_barrier(0);
         // lane holds row my_row, keys kb0 + kb*32 + (r/4)*8 + hh*4 + r%4 (raw dot products)
         if (MASK) {
+            // key kb0 + off + hh*4 is masked when it lies past the row's position (or the row is padding): one
+            // compare of the compile-time offset against a per-lane limit, then one select, per score
+            const int lim = row_valid ? my_pos - kb0 - hh * 4 : -1;
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const int key = kb0 + kb * 32 + (r >> 2) * 8 + hh * 4 + (r & 3);
-                    if (!row_valid || key > my_pos) sacc[kb][r] = -INFINITY;
+                    const int off = kb * 32 + (r >> 2) * 8 + (r & 3);
+                    if (off > lim) sacc[kb][r] = -INFINITY;
                 }
         }
         auto row_max = [&]() {
