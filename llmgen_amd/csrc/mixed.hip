@@ -9,16 +9,16 @@
 // how the dispatcher hands out the work.
 //
 // Roles come in groups of nkv workgroups (one per KV head, so every workgroup of one KV head lands on the same
-// XCD, as in the separate kernels), in a repeating pattern of one prefill group then three decode-row groups
-// while both kinds last, then whatever is left.  An XCD hands consecutive workgroups to its CUs in turn, so a
-// pattern whose period divides the XCD's 32 CUs gives each CU one role: a quarter of the CUs run prefill units
+// XCD, as in the separate kernels), in a repeating pattern of nine prefill groups then twenty-three decode-row
+// groups while both kinds last, then whatever is left.  An XCD hands consecutive workgroups to its CUs in turn,
+// so a pattern whose period divides the XCD's 32 CUs gives each CU one role: 9 of every 32 CUs run prefill units
 // (two per CU, as the prefill kernel alone) and the rest stream decode rows, which need the memory system more
 // than compute units.  On c4 (8 chunks of 512 rows beside 248 decode rows) per-workgroup timelines show both roles
-// ending within a few microseconds of each other: 193.5 us, against 227 us for the two-kernel form, 165 us for
+// ending within a few microseconds of each other: 188.6 us, against 227 us for the two-kernel form, 165 us for
 // the decode rows alone and 54 us for the chunks alone.  Measured alternatives: prefill first (its units fill
 // every CU and the decode rows wait: 229 us), one-to-one alternation (201 us), blocks of 32 groups so that every
 // CU holds one workgroup of each role (200 us: a decode row beside a prefill unit streams slower than two decode
-// rows), and prefill shares between 1/4 and 1/3 of the CUs (192.6-194.6 us).  Within each role the work goes
+// rows), and other prefill shares (same box: 1:3 190.4 us, 5:11 190.0 us, 3:5 190.8 us).  Within each role the work goes
 // heaviest first: prefill units from the end of the multi-row part of the list (the executor lists tiles lightest
 // first) and decode rows longest context first.
 //
@@ -40,7 +40,7 @@ using llmgen_prefill::PrefillLds;
 constexpr int MIX_NW = 4;  // waves per workgroup, both roles: prefill units of two heads, decode rows of 64-token
                            // wave rounds
 constexpr int MIX_NT = 4;
-constexpr int MIX_PF = 1, MIX_DEC = 3;  // role pattern: prefill groups, then decode-row groups, per period
+constexpr int MIX_PF = 9, MIX_DEC = 23;  // role pattern: prefill groups, then decode-row groups, per period
 
 template <int G>
 constexpr size_t mixed_lds_bytes() {
