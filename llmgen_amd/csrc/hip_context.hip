@@ -57,7 +57,8 @@ void llmgen_join_side_stream(hipStream_t side) {
 // Run-time options of the launchers (hip_attn_set_option).  Defaults come from the environment on first use:
 // SV_ATTN_PART (the reference's switch, attention.cu:219-229: the split-K part length is raised to at least this
 // many tokens), LLMGEN_DECODE_ROW_WAVES (4 or 8 waves per workgroup for the decode rows of a prefill step) and
-// LLMGEN_DECODE_MERGE (1: merge split-K partials in the separate merge kernel instead of in the decode kernel).
+// LLMGEN_DECODE_MERGE (1: merge split-K partials in the separate merge kernel instead of in the decode kernel) and
+// LLMGEN_PREFILL_SPLIT_TILES (heavy tiles of a pure prefill step split over two workgroups; -1 = automatic).
 static int g_opts[LLMGEN_OPT_COUNT];
 static bool g_opts_loaded = false;
 
