@@ -477,20 +477,74 @@ __device__ __forceinline__ void decode_split_body(bf16_t *__restrict__ out, floa
     // acquire at agent scope: the other workgroups' partials, published before their ticket increments, are read
     // after this point (the loads below are agent-scope atomics as well)
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    // These device-coherent loads are served from memory, so the merge is written to pay few load latencies (read
+    // one part at a time, a 32-part merge took ~30 us).  Up to MB parts: each output loads the (m, l, o) of all
+    // parts at once.  More parts: the whole workgroup first loads every (m, l) of the np parts and G heads into the
+    // LDS that the wave merge above has finished with, then each output reads its o values in batches of MB2
+    // parts, all loads of a batch issued before any is used.  Either way the arithmetic and its order are those of
+    // a part-by-part loop: M = the max over the parts, then w = 2^(m_p - M), num += w o_p, den += w l_p for
+    // p = 0, 1, ...
+    constexpr int MB = 16, MB2 = 32;
+    auto ld = [](const float *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+    float *mlb = &o_lds[0][0][0];  // [g][p][m, l]
+    const bool staged = np > MB && np * 2 <= W * HD;
+    if (staged) {
+        for (int i = tid; i < G * np; i += NTH) {
+            const int g = i / np, p = i - g * np;
+            const float *ml = part_ml + ((long)s * nq + (long)kvh * G + g) * max_parts * 2 + 2 * p;
+            mlb[2 * i] = ld(ml);
+            mlb[2 * i + 1] = ld(ml + 1);
+        }
+        __syncthreads();
+    }
     for (int idx = tid; idx < G * HD; idx += NTH) {
         const int g = idx / HD, d = idx % HD;
         const long h = (long)kvh * G + g;
-        float *ml = part_ml + ((long)s * nq + h) * max_parts * 2;
-        float *po = part_o + ((long)s * nq + h) * max_parts * HD + d;
-        float M = -INFINITY;
-        for (int p = 0; p < np; ++p)
-            M = fmaxf(M, __hip_atomic_load(ml + 2 * p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-        float num = 0.f, den = 0.f;
-        for (int p = 0; p < np; ++p) {
-            const float w =
-                fast_exp2(__hip_atomic_load(ml + 2 * p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - M);
-            num += w * __hip_atomic_load(po + (long)p * HD, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            den += w * __hip_atomic_load(ml + 2 * p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const float *ml = part_ml + ((long)s * nq + h) * max_parts * 2;
+        const float *po = part_o + ((long)s * nq + h) * max_parts * HD + d;
+        float M = -INFINITY, num = 0.f, den = 0.f;
+        if (np <= MB) {
+            float mv[MB], lv[MB], ov[MB];
+#pragma unroll
+            for (int j = 0; j < MB; ++j) {
+                const bool ok = j < np;
+                mv[j] = ok ? ld(ml + 2 * j) : -INFINITY;
+                lv[j] = ok ? ld(ml + 2 * j + 1) : 0.f;
+                ov[j] = ok ? ld(po + (long)j * HD) : 0.f;
+            }
+#pragma unroll
+            for (int j = 0; j < MB; ++j) M = fmaxf(M, mv[j]);
+#pragma unroll
+            for (int j = 0; j < MB; ++j) {
+                if (j < np) {
+                    const float w = fast_exp2(mv[j] - M);
+                    num += w * ov[j];
+                    den += w * lv[j];
+                }
+            }
+        } else if (staged) {
+            const float *mlg = mlb + 2 * g * np;
+            for (int p = 0; p < np; ++p) M = fmaxf(M, mlg[2 * p]);
+            for (int p0 = 0; p0 < np; p0 += MB2) {
+                float ov[MB2];
+#pragma unroll
+                for (int j = 0; j < MB2; ++j) ov[j] = p0 + j < np ? ld(po + (long)(p0 + j) * HD) : 0.f;
+#pragma unroll
+                for (int j = 0; j < MB2; ++j) {
+                    if (p0 + j < np) {
+                        const float w = fast_exp2(mlg[2 * (p0 + j)] - M);
+                        num += w * ov[j];
+                        den += w * mlg[2 * (p0 + j) + 1];
+                    }
+                }
+            }
+        } else {  // more parts than the LDS holds: part by part
+            for (int p = 0; p < np; ++p) M = fmaxf(M, ld(ml + 2 * p));
+            for (int p = 0; p < np; ++p) {
+                const float w = fast_exp2(ld(ml + 2 * p) - M);
+                num += w * ld(po + (long)p * HD);
+                den += w * ld(ml + 2 * p + 1);
+            }
         }
         out[((long)s * nq + h) * HD + d] = __builtin_bit_cast(bf16_t, (__bf16)(num / den));
     }
