@@ -158,7 +158,8 @@ PREFILL_KERNELS = {1: "attn_mixed_kernel (prefill units and decode rows as workg
                    2: "attn_prefill_kernel<8, *, 2> (key split in the workgroup)",
                    3: "attn_prefill_kernel<2, *, 1>", 4: "attn_prefill_kernel<4, *, 1>",
                    5: "attn_prefill_kernel<8, *, 1>",
-                   6: "attn_prefill_split_kernel (heaviest tiles' units over two workgroups)"}
+                   6: "attn_prefill_split_kernel (heaviest tiles' units over two workgroups)",
+                   7: "attn_prefill_pieces_kernel (each unit's key tiles over up to 8 workgroups)"}
 
 
 def bench_qk_fused(name: str, iters: int) -> dict:

@@ -122,6 +122,7 @@ enum {
     LLMGEN_PREFILL_W4 = 4,        /* 4-wave workgroups, two heads */
     LLMGEN_PREFILL_W8 = 5,        /* 8-wave workgroups, four heads */
     LLMGEN_PREFILL_SPLIT = 6,     /* 4-wave workgroups, the heaviest tiles' units split over two workgroups */
+    LLMGEN_PREFILL_PIECES = 7,    /* 4-wave workgroups, each unit's key tiles split over up to 8 workgroups */
     LLMGEN_PREFILL_ROWS_LAUNCH = 16
 };
 int hip_attn_prefill_plan(int n_tiles, int nq, int nkv, int hd, int block_size, int single_rows);

@@ -167,6 +167,61 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
     if (threadIdx.x == 0) __hip_atomic_store(counters + bid, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// ---- pure prefill of few units: each unit's key tiles over several workgroups ----
+//
+// A pure prefill step of at most CUs / 4 units (tile x KV head x head pair) -- a chunk of a long prompt against its
+// cached keys, a short prompt -- leaves most of the chip idle with one workgroup per unit: a 512-row chunk at
+// GQA 2 against 32K cached keys is 64 units of 520 key tiles, one chain each on 64 of 256 CUs (460 us).  Here each
+// unit gets P workgroups (P = min(8, 2 CUs / units), so all are resident at once); a unit of n key tiles uses
+// min(P, ceil(n / 4)) of them, each a contiguous equal share of its key tiles, and the others exit.  A unit with
+// one piece stores its rows directly; otherwise every piece leaves its partial (O, m, l) in the library's scratch
+// array (shared with the heavy-tile split) and the last to finish, by a ticket on a per-unit counter, merges them
+// in piece order, so the output is bit-reproducible.  The unit index runs fastest in the grid, so a KV head's
+// workgroups stay on one XCD.
+constexpr int PIECES_MAX = 8, PIECE_MIN_TILES = 4;
+
+template <int MODE>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+    attn_prefill_pieces_kernel(bf16_t *__restrict__ out, const bf16_t *__restrict__ q, const bf16_t *__restrict__ kc,
+                               const bf16_t *__restrict__ vc, const int *__restrict__ block_tables,
+                               const int *__restrict__ ctx_lens, const int *__restrict__ cu_q,
+                               const int *__restrict__ tile_seq, const int *__restrict__ tile_q0, int n_tiles, int nq,
+                               int nkv, int G, int head_groups, int max_blocks, int block_size, int bs_shift,
+                               float scale_log2, int n_units, int P, float *__restrict__ part,
+                               int *__restrict__ counters) {
+    __shared__ __attribute__((aligned(16))) unsigned char lds[sizeof(PrefillLds<4, 1>)];
+    __shared__ int s_last;
+    const int unit = (int)(blockIdx.x % (unsigned)n_units), piece = (int)(blockIdx.x / (unsigned)n_units);
+    auto body = [&](int j0, int j1, float *dst) {
+        prefill_body<4, MODE, 1, true>(out, q, kc, vc, block_tables, ctx_lens, cu_q, tile_seq, tile_q0, n_tiles, nq,
+                                      nkv, G, head_groups, max_blocks, block_size, bs_shift, scale_log2, unit, lds,
+                                      j0, j1, dst);
+    };
+    const int tile = n_tiles - 1 - unit / (nkv * head_groups);
+    const int s = tile_seq[tile], q_len = cu_q[s + 1] - cu_q[s], ctx = ctx_lens[s];
+    const int n = q_len > 1 && ctx >= q_len ? (ctx - q_len + min(tile_q0[tile] + BQ, q_len) + BK - 1) / BK : 0;
+    const int pe = n < 2 ? 1 : min(P, (n + PIECE_MIN_TILES - 1) / PIECE_MIN_TILES);
+    if (piece >= pe) return;
+    if (pe == 1) {  // one piece (also padding and single-row segments): the whole unit, rows stored directly
+        body(0, -1, nullptr);
+        return;
+    }
+    const int j0 = (int)((long)piece * n / pe), j1 = (int)((long)(piece + 1) * n / pe);
+    float *mine = part + ((long)unit * P + piece) * PART_FLOATS;
+    body(j0, j1, mine);
+    // publish (device-coherent stores, complete before the barrier), then draw a ticket: the last piece merges
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0)
+        s_last = __hip_atomic_fetch_add(counters + unit, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == pe - 1;
+    __syncthreads();
+    if (!s_last) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    prefill_merge_store_n<PIECES_MAX>(out, cu_q, tile_seq, tile_q0, n_tiles, nq, nkv, G, head_groups, unit,
+                                      part + (long)unit * P * PART_FLOATS, pe);
+    if (threadIdx.x == 0) __hip_atomic_store(counters + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <typename T>
 T *symbol_address(const T &sym) {
     static T *ptr[64] = {};
@@ -224,6 +279,36 @@ bool launch_prefill_split(int mode, bf16_t *out, const bf16_t *q, const bf16_t *
     return true;
 }
 
+// Pieces per unit for a pure prefill step of `units` units (0: the step has too many units for this launch).
+int prefill_pieces(long units) {
+    const int cus = llmgen_num_cus();
+    if (units <= 0 || units * 4 > cus || units > SPLIT_MAX_UNITS) return 0;
+    const long p = std::min<long>({(long)PIECES_MAX, 2L * cus / units, 2L * SPLIT_MAX_UNITS / units});
+    return p >= 2 ? (int)p : 0;
+}
+
+bool launch_prefill_pieces(int mode, bf16_t *out, const bf16_t *q, const bf16_t *kc, const bf16_t *vc,
+                           const int *bt, const int *ctx, const int *cu_q, const int *tile_seq, const int *tile_q0,
+                           int n_tiles, int nq, int nkv, int G, int max_blocks, int block_size, int bs_shift,
+                           float sl2) {
+    const int head_groups = G / 2;
+    const long units = (long)n_tiles * nkv * head_groups;
+    const int P = prefill_pieces(units);
+    if (P <= 0) return false;
+    float *part = reinterpret_cast<float *>(symbol_address(HIP_SYMBOL(g_split_part)));
+    int *counters = reinterpret_cast<int *>(symbol_address(HIP_SYMBOL(g_split_counters)));
+    if (!part || !counters) return false;
+    auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, dim3((unsigned)(units * P)), dim3(256), 0, g_llmgen_stream, out, q, kc, vc, bt, ctx,
+                           cu_q, tile_seq, tile_q0, n_tiles, nq, nkv, G, head_groups, max_blocks, block_size,
+                           bs_shift, sl2, (int)units, P, part, counters);
+    };
+    if (mode == DMA_BLOCK) go(attn_prefill_pieces_kernel<DMA_BLOCK>);
+    else if (mode == DMA_ROW4) go(attn_prefill_pieces_kernel<DMA_ROW4>);
+    else go(attn_prefill_pieces_kernel<DMA_FLAT>);
+    return true;
+}
+
 }  // namespace
 
 extern "C" int hip_attn_prefill_tile(void) { return BQ; }
@@ -265,7 +350,9 @@ PrefillPlan plan_prefill(int n_tiles, int G, int nkv, int single_rows) {
         // single prompts: 64 against 75 us at 3584 tokens, even at 4608).  Larger steps are bound by throughput,
         // where the 4-wave workgroups (two per CU) are faster (5632 tokens: 137 against 148 us; 16384: 986 against
         // 1069 us).  With decode rows beside it a 128 KB workgroup finds no room next to the decode kernel's waves.
-        p.kernel = single_rows == 0 && (long)n_tiles * nkv * head_groups * 2 <= 5L * llmgen_num_cus()
+        p.kernel = single_rows == 0 && prefill_pieces((long)n_tiles * nkv * head_groups) > 0
+                       ? LLMGEN_PREFILL_PIECES
+                   : single_rows == 0 && (long)n_tiles * nkv * head_groups * 2 <= 5L * llmgen_num_cus()
                        ? LLMGEN_PREFILL_KEYSPLIT
                        : (single_rows == 0 && G == 2 && split_heavy_tiles(n_tiles, nkv, head_groups) > 0
                               ? LLMGEN_PREFILL_SPLIT
@@ -322,12 +409,17 @@ extern "C" void hip_attn_prefill_rows(bf16_t *out, const bf16_t *q, const bf16_t
                                       nkv, max_blocks, block_size, scale, side);
     }
     PrefillPlan run = plan;
+    if (plan.kernel == LLMGEN_PREFILL_PIECES &&
+        !launch_prefill_pieces(mode, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq, tile_q0,
+                               n_tiles, nq, nkv, G, max_blocks, block_size, bs_shift, sl2))
+        run.kernel = LLMGEN_PREFILL_KEYSPLIT;
     if (plan.kernel == LLMGEN_PREFILL_SPLIT &&
         !launch_prefill_split(mode, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq, tile_q0,
                               n_tiles, nq, nkv, G, max_blocks, block_size, bs_shift, sl2))
         run.kernel = LLMGEN_PREFILL_W4;
     switch (run.kernel) {
         case LLMGEN_PREFILL_SPLIT:
+        case LLMGEN_PREFILL_PIECES:
             break;
         case LLMGEN_PREFILL_W2:
             launch_prefill<2>(mode, head_groups, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq,

@@ -482,4 +482,70 @@ __device__ __forceinline__ void prefill_merge_store(bf16_t *__restrict__ out, co
         }
 }
 
+// prefill_merge_store for np <= NPMAX pieces known at run time, laid out PART_FLOATS apart from `base`.  The
+// pieces' (m, l) are read at once; then each piece's 64 accumulator values are read together (64 loads in flight)
+// and folded into the running sums, piece by piece in order, as prefill_merge_store combines them.  The loop over
+// the pieces stays a loop: unrolled over NPMAX with a branch per load, its code outgrew the instruction cache.
+template <int NPMAX>
+__device__ __forceinline__ void prefill_merge_store_n(bf16_t *__restrict__ out, const int *__restrict__ cu_q,
+                                                      const int *__restrict__ tile_seq,
+                                                      const int *__restrict__ tile_q0, int n_tiles, int nq, int nkv,
+                                                      int G, int head_groups, int bid, const float *base, int np) {
+    const int kvh = bid % nkv, rest = bid / nkv, hg = rest % head_groups;
+    const int tile = n_tiles - 1 - rest / head_groups;
+    const int s = tile_seq[tile], q0 = tile_q0[tile];
+    const int q_beg = cu_q[s], q_len = cu_q[s + 1] - q_beg;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int head = kvh * G + hg * 2 + (wave >> 1);
+    const int r0 = q0 + (wave & 1) * 32, l32 = lane & 31, hh = lane >> 5;
+    if (r0 >= q_len) return;  // an inactive wave left no partial
+    auto ld = [&](const float *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+    const float *pw = base + wave * PART_WAVE_FLOATS + lane;
+    float mv[NPMAX], lv[NPMAX];
+#pragma unroll
+    for (int p = 0; p < NPMAX; ++p) {
+        const int pp = min(p, np - 1);  // no branch: pieces past np reread the last one and are not used
+        mv[p] = ld(pw + (long)pp * PART_FLOATS + 64 * 64);
+        lv[p] = ld(pw + (long)pp * PART_FLOATS + 65 * 64);
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (int p = 0; p < NPMAX; ++p)
+        if (p < np) M = fmaxf(M, mv[p]);
+    const float Mu = M == -INFINITY ? 0.f : M;
+    float o[64], l = 0.f;
+#pragma unroll
+    for (int v = 0; v < 64; ++v) o[v] = 0.f;
+    for (int p = 0; p < np; ++p) {
+        float c = 0.f, lp = 0.f;
+#pragma unroll
+        for (int i = 0; i < NPMAX; ++i)
+            if (i == p) {
+                c = fast_exp2(mv[i] - Mu);
+                lp = lv[i];
+            }
+        l += lp * c;
+        const float *src = pw + (long)p * PART_FLOATS;
+        float x[64];
+#pragma unroll
+        for (int v = 0; v < 64; ++v) x[v] = ld(src + v * 64);
+#pragma unroll
+        for (int v = 0; v < 64; ++v) o[v] += x[v] * c;
+    }
+    const float l_tot = l + lane_xor(l, 32);
+    const int my_row = r0 + l32;
+    if (my_row >= q_len) return;
+    const float inv = 1.f / l_tot;
+    bf16_t *orow = out + ((long)(q_beg + my_row) * nq + head) * HD + hh * 4;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            u32x2_t w;
+            w[0] = pack_bf16x2(o[db * 16 + rr * 4 + 0] * inv, o[db * 16 + rr * 4 + 1] * inv);
+            w[1] = pack_bf16x2(o[db * 16 + rr * 4 + 2] * inv, o[db * 16 + rr * 4 + 3] * inv);
+            *reinterpret_cast<u32x2_t *>(orow + db * 32 + rr * 8) = w;
+        }
+}
+
 }  // namespace llmgen_prefill

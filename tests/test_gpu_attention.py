@@ -356,7 +356,7 @@ def test_prefill_rows_hint_matches_unknown_count(gpu, name):
     With a count > 0 the step runs as one launch of the mixed-step kernel at GQA 2 and 4 (cpu_mixed, bs48, bs6, c4)
     and as the same two kernels otherwise (gqa8): bit-identical either way, since every workgroup role computes its
     rows as the separate kernels do.  With 0 (a pure prefill step: no decode-row launch) a small step of GQA >= 2
-    runs the key-split prefill kernel instead, which sums the keys in another order: both outputs are checked
+    runs the key-split or pieces kernel instead, which sums the keys in another order: both outputs are checked
     against the oracle (sampled rows); GQA 1 stays bit-identical."""
     wl = make(name)
     print(f"[gpu-test] {name}", flush=True)
@@ -394,9 +394,10 @@ def test_prefill_rows_hint_matches_unknown_count(gpu, name):
 def test_prefill_plan_names_the_kernel_each_config_runs(gpu):
     """hip_attn_prefill_plan reports the launch hip_attn_prefill_rows makes, from the same rule: mixed steps at
     GQA 2 / 4 with a known single-row count run one mixed-step launch, c3 (99 tiles x 8 KV heads = 792 units of two
-    heads, above 2.5 per CU) the 4-wave kernel, c5p (GQA 4, 256 tiles) the 8-wave four-head kernel, the small
-    pure prefills the key-split kernel, and an unknown count adds the separate decode-row launch; c3 (792 two-head
-    units, 3.1 per CU) splits its heaviest tiles' units over two workgroups each."""
+    heads, above 2.5 per CU) the 4-wave kernel, c5p (GQA 4, 256 tiles) the 8-wave four-head kernel, pure prefills
+    of at most a quarter unit per CU (kt_prefill) the pieces kernel, larger small ones the key-split kernel, and an
+    unknown count adds the separate decode-row launch; c3 (792 two-head units, 3.1 per CU) splits its heaviest
+    tiles' units over two workgroups each."""
     L = lib()
     pf = L.hip_attn_prefill_tile()
     plan = {}
@@ -405,11 +406,16 @@ def test_prefill_plan_names_the_kernel_each_config_runs(gpu):
         m = wl.meta(pf)
         plan[name] = (L.hip_attn_prefill_plan(m.n_tiles, wl.nq, wl.nkv, wl.hd, wl.block_size, m.single_rows()),
                       L.hip_attn_prefill_plan(m.n_tiles, wl.nq, wl.nkv, wl.hd, wl.block_size, -1))
-    MIXED, KEYSPLIT, W2, W4, W8, SPLIT, ROWS = 1, 2, 3, 4, 5, 6, 16
+    MIXED, KEYSPLIT, W2, W4, W8, SPLIT, PIECES, ROWS = 1, 2, 3, 4, 5, 6, 7, 16
     assert plan["c3"] == (SPLIT, W4 | ROWS)
     assert plan["c4"] == (MIXED, W4 | ROWS)
     assert plan["c5p"] == (W8, W8 | ROWS)
-    assert plan["kt_prefill"] == (KEYSPLIT, W4 | ROWS)
+    assert plan["kt_prefill"] == (PIECES, W4 | ROWS)
+    # pure prefill at GQA 2, 8 KV heads, 256 CUs: up to 64 units the pieces kernel, then the key split
+    if torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        assert L.hip_attn_prefill_plan(8, 16, 8, 128, 256, 0) == PIECES
+        assert L.hip_attn_prefill_plan(9, 16, 8, 128, 256, 0) == KEYSPLIT
+        assert L.hip_attn_prefill_plan(20, 16, 8, 128, 256, 0) == KEYSPLIT
     assert plan["gqa8"] == (W8 | ROWS, W8 | ROWS)
     assert plan["gqa1"] == (W2 | ROWS, W2 | ROWS)
     assert plan["cpu_mixed"][0] == MIXED and plan["bs48"][0] == MIXED
@@ -577,8 +583,8 @@ def test_pure_prefill_graph_replay(gpu, name):
     """A pure prefill step at GQA 2 (no decode-row launch) captured into a graph: three replays with eager torch
     work between them each give the eager step's output bit for bit.  c3 (792 two-head units, above the key-split
     rule's 2.5 per CU) runs the 4-wave kernel with its heaviest units split over two workgroups (halves merged
-    through the library's scratch, their ticket counters back at 0 after every launch), kt_prefill (2 tiles) the
-    key-split kernel."""
+    through the library's scratch, their ticket counters back at 0 after every launch), kt_prefill (2 tiles, 4
+    units) the pieces kernel."""
     wl = make(name)
     print(f"[gpu-test] pure prefill graph {name}", flush=True)
     t = wl.tensors(device="cuda")
@@ -586,7 +592,7 @@ def test_pure_prefill_graph_replay(gpu, name):
     L = lib()
     meta = wl.meta(L.hip_attn_prefill_tile())
     assert not meta.decode and meta.single_rows() == 0 and wl.nq // wl.nkv == 2
-    want = {"c3": 6, "kt_prefill": 2}[name]  # LLMGEN_PREFILL_SPLIT, LLMGEN_PREFILL_KEYSPLIT
+    want = {"c3": 6, "kt_prefill": 7}[name]  # LLMGEN_PREFILL_SPLIT, LLMGEN_PREFILL_PIECES
     assert L.hip_attn_prefill_plan(meta.n_tiles, wl.nq, wl.nkv, wl.hd, wl.block_size, 0) == want
     ws = wl.workspace()
     mgr = A.PagedAttentionManager()

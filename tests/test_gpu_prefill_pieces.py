@@ -1,0 +1,61 @@
+"""Pure prefill steps of few units (at most a quarter of a unit -- query tile x KV head x head pair -- per CU), which
+run the pieces kernel: each unit's key tiles split over up to 8 workgroups whose partial results the last one to
+finish merges in piece order.  Chunks of one sequence against long cached contexts reach the full 8 pieces;
+sampled rows against the oracle (max-abs 2e-2, rel-L2 1e-2), the KV cache bit for bit, and two runs of the same
+step bit-identical."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from harness import assert_cache_equal, compare, run_gpu, run_oracle
+from llmgen_amd._lib import lib
+from llmgen_amd.step import Entry
+from llmgen_amd.workloads import Workload, _tables, to_u16
+
+PIECES = 7  # LLMGEN_PREFILL_PIECES
+
+# (q heads, kv heads, block size, [(cached keys, chunk rows), ...])
+SHAPES = {
+    "g2_512_on_32k": (16, 8, 256, [(32256, 512)]),
+    "g2_200_on_5k_bs48": (4, 2, 48, [(4800, 200)]),
+    "g4_256_on_8k": (32, 8, 256, [(7936, 256)]),
+    "g2_two_chunks_bs16": (16, 8, 16, [(3000, 130), (900, 64)]),
+}
+
+
+def _workload(name):
+    nq, nkv, bs, spec = SHAPES[name]
+    rng = np.random.default_rng(len(name))
+    ctxs = [a + b for a, b in spec]
+    tables, nb = _tables(rng, ctxs, bs, permute=True, extra_blocks=2)
+    mb = max(len(t) for t in tables)
+    return Workload(name, nq, nkv, 128, bs, nb, mb, mb * bs, [Entry(a, b, t) for (a, b), t in zip(spec, tables)],
+                    std=1.0, seed=len(name) + 100, decode=False)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", list(SHAPES))
+def test_pieces_prefill_matches_oracle(gpu, name):
+    wl = _workload(name)
+    print(f"[gpu-test] pieces {name}", flush=True)
+    m = wl.meta(lib().hip_attn_prefill_tile())
+    assert m.single_rows() == 0
+    if torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        assert lib().hip_attn_prefill_plan(m.n_tiles, wl.nq, wl.nkv, wl.hd, wl.block_size, 0) == PIECES
+    t = wl.tensors(device="cuda")
+    out, kc, vc = run_gpu(wl, t)
+    out2, _, _ = run_gpu(wl, t)
+    np.testing.assert_array_equal(to_u16(out2), to_u16(out), err_msg=f"{name}: two runs differ")
+    n = m.n_tok
+    rows = np.arange(n, dtype=np.int32)
+    if n > 96:  # the first and last rows of every tile plus a seeded sample
+        picks = set(np.random.default_rng(7).integers(0, n, size=48).tolist())
+        for q0 in range(0, n, 64):
+            picks.update((q0, min(q0 + 63, n - 1)))
+        rows = np.array(sorted(picks), dtype=np.int32)
+    okc, ovc, _, of = run_oracle(wl, t, rows=rows, threads=16)
+    assert_cache_equal(to_u16(kc), okc, f"{name} K")
+    assert_cache_equal(to_u16(vc), ovc, f"{name} V")
+    compare(to_u16(out)[rows], of, name)

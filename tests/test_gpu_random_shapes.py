@@ -11,6 +11,7 @@ from __future__ import annotations
 
 import numpy as np
 import pytest
+import torch
 
 from harness import assert_cache_equal, compare, run_gpu, run_oracle
 from llmgen_amd._lib import lib
@@ -56,7 +57,8 @@ PREFILL_CASES = list(range(8))
 
 
 def _random_prefill_workload(case: int) -> Workload:
-    """Pure prefill steps (fresh prompts and chunked tails, no decode rows) at GQA 2: the key-split kernel's path.
+    """Pure prefill steps (fresh prompts and chunked tails, no decode rows) at GQA 2: the paths of the pieces and
+    key-split kernels.
     Prompt lengths cross 1, 2 and many key tiles, odd and even tile counts, and tiles that straddle blocks."""
     rng = np.random.default_rng(2000 + case)
     nkv = int(rng.choice([1, 2, 4, 8]))
@@ -81,8 +83,12 @@ def test_random_gqa2_prefill_matches_oracle(gpu, case):
     wl = _random_prefill_workload(case)
     print(f"[gpu-test] {wl.name}: {wl.note}", flush=True)
     m = wl.meta(64)
-    assert m.single_rows() == 0  # a pure prefill step: the key-split kernel runs (small steps)
-    assert lib().hip_attn_prefill_plan(m.n_tiles, wl.nq, wl.nkv, wl.hd, wl.block_size, 0) == 2
+    # a pure prefill step: up to a quarter unit (tile x KV head) per CU the pieces kernel (LLMGEN_PREFILL_PIECES,
+    # cases 0, 1, 5, 6, 7 on 256 CUs), else the key-split kernel (LLMGEN_PREFILL_KEYSPLIT, cases 2, 3, 4)
+    assert m.single_rows() == 0
+    units, cus = m.n_tiles * wl.nkv, torch.cuda.get_device_properties(0).multi_processor_count
+    want = 7 if units * 4 <= cus else 2
+    assert lib().hip_attn_prefill_plan(m.n_tiles, wl.nq, wl.nkv, wl.hd, wl.block_size, 0) == want
     t = wl.tensors(device="cuda")
     out, kc, vc = run_gpu(wl, t)
     okc, ovc, _, of = run_oracle(wl, t, threads=16)
