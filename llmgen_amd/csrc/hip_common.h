@@ -86,6 +86,11 @@ __device__ __forceinline__ u32x4_t ld16(const void *p) { return *reinterpret_cas
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Internal: the library's prefill scratch (partial results of key-range pieces, 512 slots of PART_FLOATS floats,
+// and one ticket counter per unit, zero between launches), shared by the heavy-tile split, the pieces kernel and the
+// mixed-step kernel's split prefill units; false if its address cannot be taken or `units` exceeds its counters.
+__attribute__((visibility("hidden"))) bool llmgen_prefill_scratch(float **part, int **counters, long units);
+
 // Internal (not exported): decode rows (segments with q_len == 1) of a prefill / mixed step, streamed by the
 // split-K decode kernel; defined in decode.hip, launched by hip_attn_prefill.
 __attribute__((visibility("hidden"))) void llmgen_decode_rows_of_prefill(

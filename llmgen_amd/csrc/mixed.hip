@@ -30,6 +30,8 @@
 #include "hip_common.h"
 #include "prefill_kernel.h"
 
+#include <algorithm>
+
 namespace {
 
 using llmgen_decode::decode_split_body;
@@ -41,6 +43,7 @@ constexpr int MIX_NW = 4;  // waves per workgroup, both roles: prefill units of 
                            // wave rounds
 constexpr int MIX_NT = 4;
 constexpr int MIX_PF = 9, MIX_DEC = 23;  // role pattern: prefill groups, then decode-row groups, per period
+constexpr int MIX_PIECES_MAX = 8, MIX_PIECE_TILES = 16;  // prefill units split over pieces (few long units)
 
 template <int G>
 constexpr size_t mixed_lds_bytes() {
@@ -58,10 +61,13 @@ __global__ void __launch_bounds__(64 * MIX_NW) __attribute__((amdgpu_waves_per_e
                       const bf16_t *__restrict__ vc, const int *__restrict__ block_tables,
                       const int *__restrict__ ctx_lens, const int *__restrict__ cu_q,
                       const int *__restrict__ tile_seq, const int *__restrict__ tile_q0, int n_rows, int n_pf,
-                      int nq, int nkv, int max_blocks, int block_size, int bs_shift, float scale_log2) {
+                      int nq, int nkv, int max_blocks, int block_size, int bs_shift, float scale_log2, int P,
+                      float *__restrict__ part, int *__restrict__ counters) {
     __shared__ __attribute__((aligned(16))) unsigned char lds[mixed_lds_bytes<G>()];
+    __shared__ int s_last;
     constexpr int HG = G / 2;  // prefill head groups of two heads
-    const long n_pf_wg = (long)n_pf * nkv * HG;
+    const long n_units = (long)n_pf * nkv * HG;
+    const long n_pf_wg = n_units * P;
     // role and index of this workgroup: groups of nkv, periods of MIX_PF prefill groups then MIX_DEC decode groups
     // while both last
     long b;
@@ -92,16 +98,43 @@ __global__ void __launch_bounds__(64 * MIX_NW) __attribute__((amdgpu_waves_per_e
                                                           nullptr, nullptr, nullptr, kvh, by, 0, n_list, lds);
     };
     if (b < n_pf_wg) {
-        // prefill part: unit b of the list's multi-row tiles, walked from the end
+        // prefill part: piece `piece` of unit `bid` of the list's multi-row tiles, walked from the end
         const int *ts = tile_seq + n_rows, *tq = tile_q0 + n_rows;
-        const int bid = (int)b, kvh = bid % nkv, rest = bid / nkv;
+        const int bid = (int)(b % n_units), piece = (int)(b / n_units), kvh = bid % nkv, rest = bid / nkv;
         const int t = n_pf - 1 - rest / HG;
         const int s = ts[t];
-        if (cu_q[s + 1] - cu_q[s] == 1) {  // a single-row tile out of place: the decode work, once per KV head
-            if (rest % HG == 0) decode(ts, n_pf, kvh, rest / HG);
+        const int q_len = cu_q[s + 1] - cu_q[s];
+        if (q_len == 1) {  // a single-row tile out of place: the decode work, once per KV head
+            if (piece == 0 && rest % HG == 0) decode(ts, n_pf, kvh, rest / HG);
             return;
         }
-        prefill(ts, tq, n_pf, bid);
+        // A launch with few prefill units (P > 1) splits each long unit's key tiles: a unit of n key tiles keeps
+        // min(P, n / 16) pieces, each a contiguous equal share, and the last piece to finish merges them in piece
+        // order from the library's scratch (the pieces kernel's scheme); shorter units run whole, as P = 1 does.
+        const int ctx = ctx_lens[s];
+        const int n = ctx >= q_len ? (ctx - q_len + min(tq[t] + llmgen_prefill::BQ, q_len) + llmgen_prefill::BK - 1) /
+                                         llmgen_prefill::BK
+                                   : 0;
+        const int pe = P > 1 ? max(1, min(P, n / MIX_PIECE_TILES)) : 1;
+        if (piece >= pe) return;
+        if (pe == 1) {
+            prefill(ts, tq, n_pf, bid);
+            return;
+        }
+        const int j0 = (int)((long)piece * n / pe), j1 = (int)((long)(piece + 1) * n / pe);
+        float *base = part + (long)bid * P * llmgen_prefill::PART_FLOATS;
+        prefill_body<MIX_NW, MODE, 1, true>(out, q, kc, vc, block_tables, ctx_lens, cu_q, ts, tq, n_pf, nq, nkv, G,
+                                            HG, max_blocks, block_size, bs_shift, scale_log2, bid, lds, j0, j1,
+                                            base + (long)piece * llmgen_prefill::PART_FLOATS);
+        __builtin_amdgcn_s_waitcnt(0);  // the partial's device-coherent stores complete before the ticket
+        __syncthreads();
+        if (threadIdx.x == 0)
+            s_last = __hip_atomic_fetch_add(counters + bid, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == pe - 1;
+        __syncthreads();
+        if (!s_last) return;
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        llmgen_prefill::prefill_merge_store_n<MIX_PIECES_MAX>(out, cu_q, ts, tq, n_pf, nq, nkv, G, HG, bid, base, pe);
+        if (threadIdx.x == 0) __hip_atomic_store(counters + bid, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
     // decode part: (row, kv head), longest context first
@@ -120,10 +153,12 @@ __global__ void __launch_bounds__(64 * MIX_NW) __attribute__((amdgpu_waves_per_e
 template <int G>
 void launch_mixed_g(int mode, bool pow2, long grid, bf16_t *out, const bf16_t *q, const bf16_t *kc, const bf16_t *vc,
                     const int *bt, const int *ctx, const int *cu_q, const int *tile_seq, const int *tile_q0,
-                    int n_rows, int n_pf, int nq, int nkv, int max_blocks, int block_size, int bs_shift, float sl2) {
+                    int n_rows, int n_pf, int nq, int nkv, int max_blocks, int block_size, int bs_shift, float sl2,
+                    int P, float *part, int *counters) {
     auto go = [&](auto kern) {
         hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * MIX_NW), 0, g_llmgen_stream, out, q, kc, vc, bt, ctx,
-                           cu_q, tile_seq, tile_q0, n_rows, n_pf, nq, nkv, max_blocks, block_size, bs_shift, sl2);
+                           cu_q, tile_seq, tile_q0, n_rows, n_pf, nq, nkv, max_blocks, block_size, bs_shift, sl2, P,
+                           part, counters);
     };
     using namespace llmgen_prefill;
     if (pow2) {
@@ -148,13 +183,23 @@ bool llmgen_mixed_step(bf16_t *out, const bf16_t *q, const bf16_t *k_cache, cons
     if ((G != 2 && G != 4) || single_rows <= 0 || single_rows > n_tiles) return false;
     const int bs_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctz(block_size) : -1;
     const int n_pf = n_tiles - single_rows;
-    const long grid = ((long)n_pf * (G / 2) + single_rows) * nkv;
+    // few prefill units (at most half a unit per CU): up to MIX_PIECES_MAX pieces each
+    const long units = (long)n_pf * (G / 2) * nkv;
+    float *part = nullptr;
+    int *counters = nullptr;
+    int P = 1;
+    if (units > 0 && units * 2 <= llmgen_num_cus() && llmgen_prefill_scratch(&part, &counters, units))
+        P = (int)std::min<long>({(long)MIX_PIECES_MAX, 2L * llmgen_num_cus() / units, 512L / units});
+    if (P < 2) P = 1;
+    const long grid = ((long)n_pf * (G / 2) * P + single_rows) * nkv;
     const float sl2 = scale * LLMGEN_LOG2E;
     if (G == 2)
         launch_mixed_g<2>(dma_mode, bs_shift >= 0, grid, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q,
-                          tile_seq, tile_q0, single_rows, n_pf, nq, nkv, max_blocks, block_size, bs_shift, sl2);
+                          tile_seq, tile_q0, single_rows, n_pf, nq, nkv, max_blocks, block_size, bs_shift, sl2, P,
+                          part, counters);
     else
         launch_mixed_g<4>(dma_mode, bs_shift >= 0, grid, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q,
-                          tile_seq, tile_q0, single_rows, n_pf, nq, nkv, max_blocks, block_size, bs_shift, sl2);
+                          tile_seq, tile_q0, single_rows, n_pf, nq, nkv, max_blocks, block_size, bs_shift, sl2, P,
+                          part, counters);
     return true;
 }

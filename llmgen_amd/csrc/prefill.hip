@@ -311,6 +311,13 @@ bool launch_prefill_pieces(int mode, bf16_t *out, const bf16_t *q, const bf16_t 
 
 }  // namespace
 
+bool llmgen_prefill_scratch(float **part, int **counters, long units) {
+    if (units > SPLIT_MAX_UNITS) return false;
+    *part = reinterpret_cast<float *>(symbol_address(HIP_SYMBOL(g_split_part)));
+    *counters = reinterpret_cast<int *>(symbol_address(HIP_SYMBOL(g_split_counters)));
+    return *part && *counters;
+}
+
 extern "C" int hip_attn_prefill_tile(void) { return BQ; }
 
 namespace {

@@ -1,8 +1,9 @@
-"""Pure prefill steps of few units (at most a quarter of a unit -- query tile x KV head x head pair -- per CU), which
+"""Prefill steps of few units (at most a quarter of a unit -- query tile x KV head x head pair -- per CU), which
 run the pieces kernel: each unit's key tiles split over up to 8 workgroups whose partial results the last one to
 finish merges in piece order.  Chunks of one sequence against long cached contexts reach the full 8 pieces;
 sampled rows against the oracle (max-abs 2e-2, rel-L2 1e-2), the KV cache bit for bit, and two runs of the same
-step bit-identical."""
+step bit-identical.  A mixed step whose prefill part is such a chunk (beside decode rows) splits it the same way
+inside the mixed-step kernel."""
 from __future__ import annotations
 
 import numpy as np
@@ -55,6 +56,43 @@ def test_pieces_prefill_matches_oracle(gpu, name):
         for q0 in range(0, n, 64):
             picks.update((q0, min(q0 + 63, n - 1)))
         rows = np.array(sorted(picks), dtype=np.int32)
+    okc, ovc, _, of = run_oracle(wl, t, rows=rows, threads=16)
+    assert_cache_equal(to_u16(kc), okc, f"{name} K")
+    assert_cache_equal(to_u16(vc), ovc, f"{name} V")
+    compare(to_u16(out)[rows], of, name)
+
+
+# one chunk against a long cached context beside decode rows: (q heads, kv heads, cached, chunk, decode contexts)
+MIXED_SHAPES = {
+    "g2_512_on_16k_with_63_rows": (16, 8, 15872, 512, 63),
+    "g4_192_on_6k_with_20_rows": (32, 8, 6000, 192, 20),
+}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", list(MIXED_SHAPES))
+def test_mixed_step_with_a_long_chunk_matches_oracle(gpu, name):
+    nq, nkv, cached, chunk, nd = MIXED_SHAPES[name]
+    rng = np.random.default_rng(nd)
+    dctx = [int(c) for c in rng.integers(100, 3000, size=nd)]
+    ctxs = [cached + chunk] + dctx
+    tables, nb = _tables(rng, ctxs, 256, permute=True, extra_blocks=2)
+    mb = max(len(t) for t in tables)
+    ents = [Entry(cached, chunk, tables[0])] + [Entry(c - 1, 1, t) for c, t in zip(dctx, tables[1:])]
+    wl = Workload(name, nq, nkv, 128, 256, nb, mb, mb * 256, ents, std=1.0, seed=nd, decode=False)
+    print(f"[gpu-test] mixed long chunk {name}", flush=True)
+    m = wl.meta(lib().hip_attn_prefill_tile())
+    assert m.single_rows() == nd
+    assert lib().hip_attn_prefill_plan(m.n_tiles, wl.nq, wl.nkv, wl.hd, wl.block_size, nd) == 1  # MIXED
+    t = wl.tensors(device="cuda")
+    out, kc, vc = run_gpu(wl, t)
+    out2, _, _ = run_gpu(wl, t)
+    np.testing.assert_array_equal(to_u16(out2), to_u16(out), err_msg=f"{name}: two runs differ")
+    n = m.n_tok
+    picks = set(range(n - nd, n)) | set(np.random.default_rng(3).integers(0, n - nd, size=40).tolist())
+    for q0 in range(0, chunk, 64):
+        picks.update((q0, min(q0 + 63, chunk - 1)))
+    rows = np.array(sorted(picks), dtype=np.int32)
     okc, ovc, _, of = run_oracle(wl, t, rows=rows, threads=16)
     assert_cache_equal(to_u16(kc), okc, f"{name} K")
     assert_cache_equal(to_u16(vc), ovc, f"{name} V")
