@@ -169,7 +169,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 
 // ---- pure prefill of few units: each unit's key tiles over several workgroups ----
 //
-// A pure prefill step of at most CUs / 4 units (tile x KV head x head pair) -- a chunk of a long prompt against its
+// A pure prefill step of at most CUs / 2 units (tile x KV head x head pair) -- a chunk of a long prompt against its
 // cached keys, a short prompt -- leaves most of the chip idle with one workgroup per unit: a 512-row chunk at
 // GQA 2 against 32K cached keys is 64 units of 520 key tiles, one chain each on 64 of 256 CUs (460 us).  Here each
 // unit gets P workgroups (P = min(8, 2 CUs / units), so all are resident at once); a unit of n key tiles uses
@@ -282,7 +282,7 @@ bool launch_prefill_split(int mode, bf16_t *out, const bf16_t *q, const bf16_t *
 // Pieces per unit for a pure prefill step of `units` units (0: the step has too many units for this launch).
 int prefill_pieces(long units) {
     const int cus = llmgen_num_cus();
-    if (units <= 0 || units * 4 > cus || units > SPLIT_MAX_UNITS) return 0;
+    if (units <= 0 || units * 2 > cus || units > SPLIT_MAX_UNITS) return 0;
     const long p = std::min<long>({(long)PIECES_MAX, 2L * cus / units, 2L * SPLIT_MAX_UNITS / units});
     return p >= 2 ? (int)p : 0;
 }

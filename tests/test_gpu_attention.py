@@ -302,12 +302,14 @@ def test_c5p_chunked_prefill_equals_tail(gpu):
     np.testing.assert_array_equal(to_u16(out_chunk), to_u16(out_full)[L - tail:])
 
 
-@pytest.mark.parametrize("tail", [1024, 1000])
+@pytest.mark.parametrize("tail", [2048, 2000])
 def test_c3_chunked_prefill_equals_tail(gpu, tail):
     """c3's 3584-token prompt alone (GQA 2, a pure prefill step: the key-split kernel), then its last `tail` tokens
-    as a chunk against the cached rest: bit-identical to the tail of the full prefill.  Key tiles sit at absolute
-    positions, so each tile goes to the same key group in both runs and every row sums the same keys in the same
-    order; 1000 is not a multiple of the 64-row tile, so the chunk's tiles start mid-tile of the full prefill."""
+    as a chunk against the cached rest (256 units: the key-split kernel again): bit-identical to the tail of the full
+    prefill.  Key tiles sit at absolute positions, so each tile goes to the same key group in both runs and every
+    row sums the same keys in the same order; 2000 is not a multiple of the 64-row tile, so the chunk's tiles start
+    mid-tile of the full prefill.  (A chunk of at most 128 units runs the pieces kernel, whose piece boundaries
+    follow the chunk: its rows match the full prefill within tolerance, not bit for bit.)"""
     import copy as _copy
 
     from llmgen_amd.step import Entry
@@ -324,6 +326,9 @@ def test_c3_chunked_prefill_equals_tail(gpu, tail):
     wl2.entries = [Entry(L - tail, tail, wl.entries[0].block_table)]
     t2 = {"q": t["q"][L - tail:].contiguous(), "k": t["k"][L - tail:].contiguous(),
           "v": t["v"][L - tail:].contiguous(), "kc": kc, "vc": vc}
+    m2 = wl2.meta(lib().hip_attn_prefill_tile())
+    if torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        assert lib().hip_attn_prefill_plan(m2.n_tiles, wl.nq, wl.nkv, wl.hd, wl.block_size, 0) == 2  # KEYSPLIT
     out_chunk, _, _ = _step(wl2, t2)
     np.testing.assert_array_equal(to_u16(out_chunk), to_u16(out_full)[L - tail:])
 
@@ -395,7 +400,7 @@ def test_prefill_plan_names_the_kernel_each_config_runs(gpu):
     """hip_attn_prefill_plan reports the launch hip_attn_prefill_rows makes, from the same rule: mixed steps at
     GQA 2 / 4 with a known single-row count run one mixed-step launch, c3 (99 tiles x 8 KV heads = 792 units of two
     heads, above 2.5 per CU) the 4-wave kernel, c5p (GQA 4, 256 tiles) the 8-wave four-head kernel, pure prefills
-    of at most a quarter unit per CU (kt_prefill) the pieces kernel, larger small ones the key-split kernel, and an
+    of at most half a unit per CU (kt_prefill) the pieces kernel, larger small ones the key-split kernel, and an
     unknown count adds the separate decode-row launch; c3 (792 two-head units, 3.1 per CU) splits its heaviest
     tiles' units over two workgroups each."""
     L = lib()
@@ -411,10 +416,10 @@ def test_prefill_plan_names_the_kernel_each_config_runs(gpu):
     assert plan["c4"] == (MIXED, W4 | ROWS)
     assert plan["c5p"] == (W8, W8 | ROWS)
     assert plan["kt_prefill"] == (PIECES, W4 | ROWS)
-    # pure prefill at GQA 2, 8 KV heads, 256 CUs: up to 64 units the pieces kernel, then the key split
+    # pure prefill at GQA 2, 8 KV heads, 256 CUs: up to 128 units the pieces kernel, then the key split
     if torch.cuda.get_device_properties(0).multi_processor_count == 256:
-        assert L.hip_attn_prefill_plan(8, 16, 8, 128, 256, 0) == PIECES
-        assert L.hip_attn_prefill_plan(9, 16, 8, 128, 256, 0) == KEYSPLIT
+        assert L.hip_attn_prefill_plan(16, 16, 8, 128, 256, 0) == PIECES
+        assert L.hip_attn_prefill_plan(17, 16, 8, 128, 256, 0) == KEYSPLIT
         assert L.hip_attn_prefill_plan(20, 16, 8, 128, 256, 0) == KEYSPLIT
     assert plan["gqa8"] == (W8 | ROWS, W8 | ROWS)
     assert plan["gqa1"] == (W2 | ROWS, W2 | ROWS)

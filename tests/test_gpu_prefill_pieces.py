@@ -1,4 +1,4 @@
-"""Prefill steps of few units (at most a quarter of a unit -- query tile x KV head x head pair -- per CU), which
+"""Prefill steps of few units (at most half a unit -- query tile x KV head x head pair -- per CU), which
 run the pieces kernel: each unit's key tiles split over up to 8 workgroups whose partial results the last one to
 finish merges in piece order.  Chunks of one sequence against long cached contexts reach the full 8 pieces;
 sampled rows against the oracle (max-abs 2e-2, rel-L2 1e-2), the KV cache bit for bit, and two runs of the same

@@ -83,11 +83,11 @@ def test_random_gqa2_prefill_matches_oracle(gpu, case):
     wl = _random_prefill_workload(case)
     print(f"[gpu-test] {wl.name}: {wl.note}", flush=True)
     m = wl.meta(64)
-    # a pure prefill step: up to a quarter unit (tile x KV head) per CU the pieces kernel (LLMGEN_PREFILL_PIECES,
-    # cases 0, 1, 5, 6, 7 on 256 CUs), else the key-split kernel (LLMGEN_PREFILL_KEYSPLIT, cases 2, 3, 4)
+    # a pure prefill step: up to half a unit (tile x KV head) per CU the pieces kernel (LLMGEN_PREFILL_PIECES,
+    # every case but 3 on 256 CUs), else the key-split kernel (LLMGEN_PREFILL_KEYSPLIT, case 3)
     assert m.single_rows() == 0
     units, cus = m.n_tiles * wl.nkv, torch.cuda.get_device_properties(0).multi_processor_count
-    want = 7 if units * 4 <= cus else 2
+    want = 7 if units * 2 <= cus else 2
     assert lib().hip_attn_prefill_plan(m.n_tiles, wl.nq, wl.nkv, wl.hd, wl.block_size, 0) == want
     t = wl.tensors(device="cuda")
     out, kc, vc = run_gpu(wl, t)
