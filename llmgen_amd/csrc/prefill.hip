@@ -169,7 +169,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 
 // ---- pure prefill of few units: each unit's key tiles over several workgroups ----
 //
-// A pure prefill step of at most CUs / 2 units (tile x KV head x head pair) -- a chunk of a long prompt against its
+// A pure prefill step of at most CUs / 2 units (tile x KV head x head pair; CUs one-head units at G = 1) -- a chunk of a long prompt against its
 // cached keys, a short prompt -- leaves most of the chip idle with one workgroup per unit: a 512-row chunk at
 // GQA 2 against 32K cached keys is 64 units of 520 key tiles, one chain each on 64 of 256 CUs (460 us).  Here each
 // unit gets P workgroups (P = min(8, 2 CUs / units), so all are resident at once); a unit of n key tiles uses
@@ -180,8 +180,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 // workgroups stay on one XCD.
 constexpr int PIECES_MAX = 8, PIECE_MIN_TILES = 4;
 
-template <int MODE>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+template <int MODE, int NW>
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)))
     attn_prefill_pieces_kernel(bf16_t *__restrict__ out, const bf16_t *__restrict__ q, const bf16_t *__restrict__ kc,
                                const bf16_t *__restrict__ vc, const int *__restrict__ block_tables,
                                const int *__restrict__ ctx_lens, const int *__restrict__ cu_q,
@@ -189,11 +189,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
                                int nkv, int G, int head_groups, int max_blocks, int block_size, int bs_shift,
                                float scale_log2, int n_units, int P, float *__restrict__ part,
                                int *__restrict__ counters) {
-    __shared__ __attribute__((aligned(16))) unsigned char lds[sizeof(PrefillLds<4, 1>)];
+    __shared__ __attribute__((aligned(16))) unsigned char lds[sizeof(PrefillLds<NW, 1>)];
     __shared__ int s_last;
+    constexpr int PSTRIDE = NW * PART_WAVE_FLOATS;  // scratch floats per piece
     const int unit = (int)(blockIdx.x % (unsigned)n_units), piece = (int)(blockIdx.x / (unsigned)n_units);
     auto body = [&](int j0, int j1, float *dst) {
-        prefill_body<4, MODE, 1, true>(out, q, kc, vc, block_tables, ctx_lens, cu_q, tile_seq, tile_q0, n_tiles, nq,
+        prefill_body<NW, MODE, 1, true>(out, q, kc, vc, block_tables, ctx_lens, cu_q, tile_seq, tile_q0, n_tiles, nq,
                                       nkv, G, head_groups, max_blocks, block_size, bs_shift, scale_log2, unit, lds,
                                       j0, j1, dst);
     };
@@ -207,7 +208,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
         return;
     }
     const int j0 = (int)((long)piece * n / pe), j1 = (int)((long)(piece + 1) * n / pe);
-    float *mine = part + ((long)unit * P + piece) * PART_FLOATS;
+    float *mine = part + ((long)unit * P + piece) * PSTRIDE;
     body(j0, j1, mine);
     // publish (device-coherent stores, complete before the barrier), then draw a ticket: the last piece merges
     __builtin_amdgcn_s_waitcnt(0);
@@ -217,8 +218,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
     __syncthreads();
     if (!s_last) return;
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    prefill_merge_store_n<PIECES_MAX>(out, cu_q, tile_seq, tile_q0, n_tiles, nq, nkv, G, head_groups, unit,
-                                      part + (long)unit * P * PART_FLOATS, pe);
+    prefill_merge_store_n<PIECES_MAX, NW>(out, cu_q, tile_seq, tile_q0, n_tiles, nq, nkv, G, head_groups, unit,
+                                          part + (long)unit * P * PSTRIDE, pe);
     if (threadIdx.x == 0) __hip_atomic_store(counters + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -279,11 +280,13 @@ bool launch_prefill_split(int mode, bf16_t *out, const bf16_t *q, const bf16_t *
     return true;
 }
 
-// Pieces per unit for a pure prefill step of `units` units (0: the step has too many units for this launch).
-int prefill_pieces(long units) {
-    const int cus = llmgen_num_cus();
-    if (units <= 0 || units * 2 > cus || units > SPLIT_MAX_UNITS) return 0;
-    const long p = std::min<long>({(long)PIECES_MAX, 2L * cus / units, 2L * SPLIT_MAX_UNITS / units});
+// Pieces per unit for a pure prefill step of `units` units of nw-wave workgroups (0: too many units for this
+// launch).  The CUs hold 8 / nw such workgroups each; a step qualifies when every unit can have at least 4.
+int prefill_pieces(long units, int nw) {
+    const long slots = (long)llmgen_num_cus() * (8 / nw);
+    const long capacity = 2L * SPLIT_MAX_UNITS * 4 / nw;  // pieces the scratch array holds
+    if (units <= 0 || units * 4 > slots || units > SPLIT_MAX_UNITS) return 0;
+    const long p = std::min<long>({(long)PIECES_MAX, slots / units, capacity / units});
     return p >= 2 ? (int)p : 0;
 }
 
@@ -291,21 +294,28 @@ bool launch_prefill_pieces(int mode, bf16_t *out, const bf16_t *q, const bf16_t 
                            const int *bt, const int *ctx, const int *cu_q, const int *tile_seq, const int *tile_q0,
                            int n_tiles, int nq, int nkv, int G, int max_blocks, int block_size, int bs_shift,
                            float sl2) {
-    const int head_groups = G / 2;
+    const int nw = G == 1 ? 2 : 4;  // one head per 2-wave workgroup at G = 1, else two per 4-wave workgroup
+    const int head_groups = G / (nw / 2);
     const long units = (long)n_tiles * nkv * head_groups;
-    const int P = prefill_pieces(units);
+    const int P = prefill_pieces(units, nw);
     if (P <= 0) return false;
     float *part = reinterpret_cast<float *>(symbol_address(HIP_SYMBOL(g_split_part)));
     int *counters = reinterpret_cast<int *>(symbol_address(HIP_SYMBOL(g_split_counters)));
     if (!part || !counters) return false;
     auto go = [&](auto kern) {
-        hipLaunchKernelGGL(kern, dim3((unsigned)(units * P)), dim3(256), 0, g_llmgen_stream, out, q, kc, vc, bt, ctx,
+        hipLaunchKernelGGL(kern, dim3((unsigned)(units * P)), dim3(64 * nw), 0, g_llmgen_stream, out, q, kc, vc, bt, ctx,
                            cu_q, tile_seq, tile_q0, n_tiles, nq, nkv, G, head_groups, max_blocks, block_size,
                            bs_shift, sl2, (int)units, P, part, counters);
     };
-    if (mode == DMA_BLOCK) go(attn_prefill_pieces_kernel<DMA_BLOCK>);
-    else if (mode == DMA_ROW4) go(attn_prefill_pieces_kernel<DMA_ROW4>);
-    else go(attn_prefill_pieces_kernel<DMA_FLAT>);
+    if (nw == 2) {
+        if (mode == DMA_BLOCK) go(attn_prefill_pieces_kernel<DMA_BLOCK, 2>);
+        else if (mode == DMA_ROW4) go(attn_prefill_pieces_kernel<DMA_ROW4, 2>);
+        else go(attn_prefill_pieces_kernel<DMA_FLAT, 2>);
+    } else {
+        if (mode == DMA_BLOCK) go(attn_prefill_pieces_kernel<DMA_BLOCK, 4>);
+        else if (mode == DMA_ROW4) go(attn_prefill_pieces_kernel<DMA_ROW4, 4>);
+        else go(attn_prefill_pieces_kernel<DMA_FLAT, 4>);
+    }
     return true;
 }
 
@@ -350,14 +360,16 @@ PrefillPlan plan_prefill(int n_tiles, int G, int nkv, int single_rows) {
     // is device data), so it is skipped when the caller knows there are none.
     p.rows_launch = single_rows != 0;
     if (p.heads_per_wg == 1) {
-        p.kernel = LLMGEN_PREFILL_W2;
+        // a pure prefill step of at most one one-head unit per CU: the pieces kernel's 2-wave form
+        p.kernel = single_rows == 0 && prefill_pieces((long)n_tiles * nkv * head_groups, 2) > 0 ? LLMGEN_PREFILL_PIECES
+                                                                                              : LLMGEN_PREFILL_W2;
     } else if (p.heads_per_wg == 2) {
         // Pure prefill of up to 2.5 units per CU: 8-wave workgroups whose two key groups split each unit's key
         // tiles, so the heaviest units (a long prompt's last tiles) take half as many iterations (measured on
         // single prompts: 64 against 75 us at 3584 tokens, even at 4608).  Larger steps are bound by throughput,
         // where the 4-wave workgroups (two per CU) are faster (5632 tokens: 137 against 148 us; 16384: 986 against
         // 1069 us).  With decode rows beside it a 128 KB workgroup finds no room next to the decode kernel's waves.
-        p.kernel = single_rows == 0 && prefill_pieces((long)n_tiles * nkv * head_groups) > 0
+        p.kernel = single_rows == 0 && prefill_pieces((long)n_tiles * nkv * head_groups, 4) > 0
                        ? LLMGEN_PREFILL_PIECES
                    : single_rows == 0 && (long)n_tiles * nkv * head_groups * 2 <= 5L * llmgen_num_cus()
                        ? LLMGEN_PREFILL_KEYSPLIT
@@ -419,7 +431,7 @@ extern "C" void hip_attn_prefill_rows(bf16_t *out, const bf16_t *q, const bf16_t
     if (plan.kernel == LLMGEN_PREFILL_PIECES &&
         !launch_prefill_pieces(mode, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq, tile_q0,
                                n_tiles, nq, nkv, G, max_blocks, block_size, bs_shift, sl2))
-        run.kernel = LLMGEN_PREFILL_KEYSPLIT;
+        run.kernel = G == 1 ? LLMGEN_PREFILL_W2 : LLMGEN_PREFILL_KEYSPLIT;
     if (plan.kernel == LLMGEN_PREFILL_SPLIT &&
         !launch_prefill_split(mode, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq, tile_q0,
                               n_tiles, nq, nkv, G, max_blocks, block_size, bs_shift, sl2))

@@ -80,7 +80,7 @@ __device__ __forceinline__ void prefill_body(bf16_t *__restrict__ out, const bf1
                         int nkv, int G, int head_groups, int max_blocks, int block_size, int bs_shift,
                         float scale_log2, int bid, unsigned char *lds, int j0 = 0, int j1 = 0,
                         float *__restrict__ part = nullptr) {
-    static_assert(!SK || (KS == 1 && NW == 4), "key ranges are for 4-wave, one-group workgroups");
+    static_assert(!SK || (KS == 1 && (NW == 4 || NW == 2)), "key ranges are for 4- or 2-wave, one-group workgroups");
     constexpr int NWG = NW / KS;     // waves per key group
     constexpr int LOADS = 16 / NWG;  // 4-row DMA instructions per wave per tile, for K and for V each
 
@@ -482,11 +482,12 @@ __device__ __forceinline__ void prefill_merge_store(bf16_t *__restrict__ out, co
         }
 }
 
-// prefill_merge_store for np <= NPMAX pieces known at run time, laid out PART_FLOATS apart from `base`.  The
+// prefill_merge_store for np <= NPMAX pieces known at run time of NW-wave workgroups (two heads at NW = 4, one at
+// NW = 2), laid out NW * PART_WAVE_FLOATS apart from `base`.  The
 // pieces' (m, l) are read at once; then each piece's 64 accumulator values are read together (64 loads in flight)
 // and folded into the running sums, piece by piece in order, as prefill_merge_store combines them.  The loop over
 // the pieces stays a loop: unrolled over NPMAX with a branch per load, its code outgrew the instruction cache.
-template <int NPMAX>
+template <int NPMAX, int NW = 4>
 __device__ __forceinline__ void prefill_merge_store_n(bf16_t *__restrict__ out, const int *__restrict__ cu_q,
                                                       const int *__restrict__ tile_seq,
                                                       const int *__restrict__ tile_q0, int n_tiles, int nq, int nkv,
@@ -496,17 +497,18 @@ __device__ __forceinline__ void prefill_merge_store_n(bf16_t *__restrict__ out, 
     const int s = tile_seq[tile], q0 = tile_q0[tile];
     const int q_beg = cu_q[s], q_len = cu_q[s + 1] - q_beg;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int head = kvh * G + hg * 2 + (wave >> 1);
+    const int head = kvh * G + hg * (NW / 2) + (wave >> 1);
     const int r0 = q0 + (wave & 1) * 32, l32 = lane & 31, hh = lane >> 5;
     if (r0 >= q_len) return;  // an inactive wave left no partial
     auto ld = [&](const float *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+    constexpr int PSTRIDE = NW * PART_WAVE_FLOATS;  // floats per piece
     const float *pw = base + wave * PART_WAVE_FLOATS + lane;
     float mv[NPMAX], lv[NPMAX];
 #pragma unroll
     for (int p = 0; p < NPMAX; ++p) {
         const int pp = min(p, np - 1);  // no branch: pieces past np reread the last one and are not used
-        mv[p] = ld(pw + (long)pp * PART_FLOATS + 64 * 64);
-        lv[p] = ld(pw + (long)pp * PART_FLOATS + 65 * 64);
+        mv[p] = ld(pw + (long)pp * PSTRIDE + 64 * 64);
+        lv[p] = ld(pw + (long)pp * PSTRIDE + 65 * 64);
     }
     float M = -INFINITY;
 #pragma unroll
@@ -525,7 +527,7 @@ __device__ __forceinline__ void prefill_merge_store_n(bf16_t *__restrict__ out, 
                 lp = lv[i];
             }
         l += lp * c;
-        const float *src = pw + (long)p * PART_FLOATS;
+        const float *src = pw + (long)p * PSTRIDE;
         float x[64];
 #pragma unroll
         for (int v = 0; v < 64; ++v) x[v] = ld(src + v * 64);

@@ -23,6 +23,7 @@ SHAPES = {
     "g2_200_on_5k_bs48": (4, 2, 48, [(4800, 200)]),
     "g4_256_on_8k": (32, 8, 256, [(7936, 256)]),
     "g2_two_chunks_bs16": (16, 8, 16, [(3000, 130), (900, 64)]),
+    "g1_512_on_16k": (16, 16, 256, [(15872, 512)]),  # GQA 1: one head per 2-wave workgroup
 }
 
 
