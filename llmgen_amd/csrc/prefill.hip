@@ -187,12 +187,26 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
                                const int *__restrict__ ctx_lens, const int *__restrict__ cu_q,
                                const int *__restrict__ tile_seq, const int *__restrict__ tile_q0, int n_tiles, int nq,
                                int nkv, int G, int head_groups, int max_blocks, int block_size, int bs_shift,
-                               float scale_log2, int n_units, int P, float *__restrict__ part,
+                               float scale_log2, int n_front, int n_units, int P, float *__restrict__ part,
                                int *__restrict__ counters) {
     __shared__ __attribute__((aligned(16))) unsigned char lds[sizeof(PrefillLds<NW, 1>)];
     __shared__ int s_last;
     constexpr int PSTRIDE = NW * PART_WAVE_FLOATS;  // scratch floats per piece
-    const int unit = (int)(blockIdx.x % (unsigned)n_units), piece = (int)(blockIdx.x / (unsigned)n_units);
+    // The list's first n_front tiles (a mixed step's single-row segments) get one workgroup per unit, which runs a
+    // multi-row tile found there whole and skips the single rows (the decode-row launch streams them); the rest of
+    // the list is split into pieces.
+    const long front_wg = (long)n_front * nkv * head_groups;
+    if (blockIdx.x < front_wg) {
+        prefill_body<NW, MODE, 1, true>(out, q, kc, vc, block_tables, ctx_lens, cu_q, tile_seq, tile_q0, n_front, nq,
+                                        nkv, G, head_groups, max_blocks, block_size, bs_shift, scale_log2,
+                                        (int)blockIdx.x, lds, 0, -1, nullptr);
+        return;
+    }
+    tile_seq += n_front;
+    tile_q0 += n_front;
+    n_tiles -= n_front;
+    const long b = blockIdx.x - front_wg;
+    const int unit = (int)(b % n_units), piece = (int)(b / n_units);
     auto body = [&](int j0, int j1, float *dst) {
         prefill_body<NW, MODE, 1, true>(out, q, kc, vc, block_tables, ctx_lens, cu_q, tile_seq, tile_q0, n_tiles, nq,
                                       nkv, G, head_groups, max_blocks, block_size, bs_shift, scale_log2, unit, lds,
@@ -290,22 +304,24 @@ int prefill_pieces(long units, int nw) {
     return p >= 2 ? (int)p : 0;
 }
 
+// n_front: tiles at the front of the list not to split (a mixed step's single-row segments), 0 for a pure step.
 bool launch_prefill_pieces(int mode, bf16_t *out, const bf16_t *q, const bf16_t *kc, const bf16_t *vc,
                            const int *bt, const int *ctx, const int *cu_q, const int *tile_seq, const int *tile_q0,
                            int n_tiles, int nq, int nkv, int G, int max_blocks, int block_size, int bs_shift,
-                           float sl2) {
+                           float sl2, int n_front) {
     const int nw = G == 1 ? 2 : 4;  // one head per 2-wave workgroup at G = 1, else two per 4-wave workgroup
     const int head_groups = G / (nw / 2);
-    const long units = (long)n_tiles * nkv * head_groups;
+    const long units = (long)(n_tiles - n_front) * nkv * head_groups;
+    const long front_wg = (long)n_front * nkv * head_groups;
     const int P = prefill_pieces(units, nw);
     if (P <= 0) return false;
     float *part = reinterpret_cast<float *>(symbol_address(HIP_SYMBOL(g_split_part)));
     int *counters = reinterpret_cast<int *>(symbol_address(HIP_SYMBOL(g_split_counters)));
     if (!part || !counters) return false;
     auto go = [&](auto kern) {
-        hipLaunchKernelGGL(kern, dim3((unsigned)(units * P)), dim3(64 * nw), 0, g_llmgen_stream, out, q, kc, vc, bt, ctx,
-                           cu_q, tile_seq, tile_q0, n_tiles, nq, nkv, G, head_groups, max_blocks, block_size,
-                           bs_shift, sl2, (int)units, P, part, counters);
+        hipLaunchKernelGGL(kern, dim3((unsigned)(front_wg + units * P)), dim3(64 * nw), 0, g_llmgen_stream, out, q,
+                           kc, vc, bt, ctx, cu_q, tile_seq, tile_q0, n_tiles, nq, nkv, G, head_groups, max_blocks,
+                           block_size, bs_shift, sl2, n_front, (int)units, P, part, counters);
     };
     if (nw == 2) {
         if (mode == DMA_BLOCK) go(attn_prefill_pieces_kernel<DMA_BLOCK, 2>);
@@ -359,6 +375,15 @@ PrefillPlan plan_prefill(int n_tiles, int G, int nkv, int single_rows) {
     // concurrently with the MFMA kernel (which skips them).  Its grid covers every tile (which tiles are single rows
     // is device data), so it is skipped when the caller knows there are none.
     p.rows_launch = single_rows != 0;
+    // A mixed step at other G whose prefill tiles (after its single rows) are few units: the pieces kernel for them,
+    // beside the decode-row launch
+    if (single_rows > 0 && single_rows < n_tiles) {
+        const int nw = G == 1 ? 2 : 4;
+        if (prefill_pieces((long)(n_tiles - single_rows) * nkv * (G / (nw / 2)), nw) > 0) {
+            p.kernel = LLMGEN_PREFILL_PIECES;
+            return p;
+        }
+    }
     if (p.heads_per_wg == 1) {
         // a pure prefill step of at most one one-head unit per CU: the pieces kernel's 2-wave form
         p.kernel = single_rows == 0 && prefill_pieces((long)n_tiles * nkv * head_groups, 2) > 0 ? LLMGEN_PREFILL_PIECES
@@ -430,8 +455,9 @@ extern "C" void hip_attn_prefill_rows(bf16_t *out, const bf16_t *q, const bf16_t
     PrefillPlan run = plan;
     if (plan.kernel == LLMGEN_PREFILL_PIECES &&
         !launch_prefill_pieces(mode, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq, tile_q0,
-                               n_tiles, nq, nkv, G, max_blocks, block_size, bs_shift, sl2))
-        run.kernel = G == 1 ? LLMGEN_PREFILL_W2 : LLMGEN_PREFILL_KEYSPLIT;
+                               n_tiles, nq, nkv, G, max_blocks, block_size, bs_shift, sl2,
+                               single_rows > 0 ? single_rows : 0))
+        run.kernel = G == 1 ? LLMGEN_PREFILL_W2 : single_rows > 0 ? LLMGEN_PREFILL_W8 : LLMGEN_PREFILL_KEYSPLIT;
     if (plan.kernel == LLMGEN_PREFILL_SPLIT &&
         !launch_prefill_split(mode, out, q, k_cache, v_cache, block_tables, ctx_lens, cu_q, tile_seq, tile_q0,
                               n_tiles, nq, nkv, G, max_blocks, block_size, bs_shift, sl2))

@@ -358,11 +358,12 @@ def test_zero_sized_launches_are_noops(gpu):
 @pytest.mark.parametrize("name", ["cpu_mixed", "bs48", "bs6", "gqa8", "c4", "c3", "kt_prefill"])
 def test_prefill_rows_hint_matches_unknown_count(gpu, name):
     """hip_attn_prefill_rows with the step's single-row segment count against hip_attn_prefill (count unknown).
-    With a count > 0 the step runs as one launch of the mixed-step kernel at GQA 2 and 4 (cpu_mixed, bs48, bs6, c4)
-    and as the same two kernels otherwise (gqa8): bit-identical either way, since every workgroup role computes its
-    rows as the separate kernels do.  With 0 (a pure prefill step: no decode-row launch) a small step of GQA >= 2
-    runs the key-split or pieces kernel instead, which sums the keys in another order: both outputs are checked
-    against the oracle (sampled rows); GQA 1 stays bit-identical."""
+    With a count > 0 the step runs as one launch of the mixed-step kernel at GQA 2 and 4 (cpu_mixed, bs48, bs6, c4),
+    bit-identical since every workgroup role computes its rows as the separate kernels do (their prefill units are
+    too short to be split).  Otherwise a known count or 0 (a pure prefill step: no decode-row launch) can select
+    another prefill kernel (the pieces kernel for gqa8's few units, the key-split or pieces kernel for small pure
+    steps), which sums the keys in another order: then both outputs are checked against the oracle (sampled
+    rows)."""
     wl = make(name)
     print(f"[gpu-test] {name}", flush=True)
     t = wl.tensors(device="cuda")
@@ -387,7 +388,9 @@ def test_prefill_rows_hint_matches_unknown_count(gpu, name):
         torch.cuda.synchronize()
         check_hip_error(name)
         outs.append(to_u16(out))
-    if meta.single_rows() == 0 and wl.nq // wl.nkv >= 2:
+    plans = [L.hip_attn_prefill_plan(meta.n_tiles, wl.nq, wl.nkv, wl.hd, wl.block_size, h)
+             for h in (-1, meta.single_rows())]
+    if (plans[1] & 15) not in (1, plans[0] & 15):  # another kernel than the mixed one or the unknown count's
         rows = _sample_rows(wl, meta)
         _, _, _, of = run_oracle(wl, t, rows=rows, threads=16)
         for o, what in zip(outs, ("unknown", "hint 0")):
@@ -421,8 +424,9 @@ def test_prefill_plan_names_the_kernel_each_config_runs(gpu):
         assert L.hip_attn_prefill_plan(16, 16, 8, 128, 256, 0) == PIECES
         assert L.hip_attn_prefill_plan(17, 16, 8, 128, 256, 0) == KEYSPLIT
         assert L.hip_attn_prefill_plan(20, 16, 8, 128, 256, 0) == KEYSPLIT
-    assert plan["gqa8"] == (W8 | ROWS, W8 | ROWS)
-    assert plan["gqa1"] == (W2 | ROWS, W2 | ROWS)
+    # GQA 8 and 1 mixed steps with a known count: their few prefill units take the pieces kernel beside the rows
+    assert plan["gqa8"] == (PIECES | ROWS, W8 | ROWS)
+    assert plan["gqa1"] == (PIECES | ROWS, W2 | ROWS)
     assert plan["cpu_mixed"][0] == MIXED and plan["bs48"][0] == MIXED
     assert L.hip_attn_prefill_plan(0, 16, 8, 128, 256, 0) == 0
     assert L.hip_attn_prefill_plan(4, 16, 8, 64, 256, 0) == -1 and L.hip_attn_prefill_plan(4, 24, 8, 128, 256, 0) == -1

@@ -3,7 +3,7 @@ run the pieces kernel: each unit's key tiles split over up to 8 workgroups whose
 finish merges in piece order.  Chunks of one sequence against long cached contexts reach the full 8 pieces;
 sampled rows against the oracle (max-abs 2e-2, rel-L2 1e-2), the KV cache bit for bit, and two runs of the same
 step bit-identical.  A mixed step whose prefill part is such a chunk (beside decode rows) splits it the same way
-inside the mixed-step kernel."""
+inside the mixed-step kernel (GQA 2, 4) or in the pieces kernel beside the decode-row launch (GQA 1, 8)."""
 from __future__ import annotations
 
 import numpy as np
@@ -67,6 +67,8 @@ def test_pieces_prefill_matches_oracle(gpu, name):
 MIXED_SHAPES = {
     "g2_512_on_16k_with_63_rows": (16, 8, 15872, 512, 63),
     "g4_192_on_6k_with_20_rows": (32, 8, 6000, 192, 20),
+    "g1_512_on_16k_with_31_rows": (16, 16, 15872, 512, 31),  # GQA 1 and 8: the pieces kernel beside the rows
+    "g8_256_on_8k_with_15_rows": (64, 8, 7936, 256, 15),
 }
 
 
@@ -84,7 +86,9 @@ def test_mixed_step_with_a_long_chunk_matches_oracle(gpu, name):
     print(f"[gpu-test] mixed long chunk {name}", flush=True)
     m = wl.meta(lib().hip_attn_prefill_tile())
     assert m.single_rows() == nd
-    assert lib().hip_attn_prefill_plan(m.n_tiles, wl.nq, wl.nkv, wl.hd, wl.block_size, nd) == 1  # MIXED
+    want = 1 if nq // nkv in (2, 4) else PIECES | 16  # MIXED, or PIECES + the decode-row launch
+    if torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        assert lib().hip_attn_prefill_plan(m.n_tiles, wl.nq, wl.nkv, wl.hd, wl.block_size, nd) == want
     t = wl.tensors(device="cuda")
     out, kc, vc = run_gpu(wl, t)
     out2, _, _ = run_gpu(wl, t)
