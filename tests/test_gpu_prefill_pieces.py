@@ -102,3 +102,44 @@ def test_mixed_step_with_a_long_chunk_matches_oracle(gpu, name):
     assert_cache_equal(to_u16(kc), okc, f"{name} K")
     assert_cache_equal(to_u16(vc), ovc, f"{name} V")
     compare(to_u16(out)[rows], of, name)
+
+
+@pytest.mark.gpu
+def test_pieces_prefill_graph_replay(gpu):
+    """The 8-piece step captured into a graph: three replays with eager torch work between them each equal the
+    eager step bit for bit (the per-unit ticket counters are back at 0 after every launch)."""
+    from harness import check_hip_error
+    from llmgen_amd import attention as A
+
+    wl = _workload("g2_512_on_32k")
+    print("[gpu-test] pieces graph replay", flush=True)
+    t = wl.tensors(device="cuda")
+    A.init_device()
+    L = lib()
+    ws = wl.workspace()
+    mgr = A.PagedAttentionManager()
+    mgr.layers[0] = A.LayerState(t["kc"].clone(), t["vc"].clone())
+    A.g_attn_mgr = mgr
+    wl.bind(ws)
+    node_out = torch.full((wl.n_tok, wl.nq, wl.hd), float("nan"), dtype=torch.bfloat16, device="cuda")
+    node = A.AttnNode(node_out, [t["q"], t["k"], t["v"]], layer_id=0)
+    A.PagedAttentionImpl.execute(0, node)
+    torch.cuda.synchronize()
+    check_hip_error("pieces eager")
+    ref = to_u16(node_out).copy()
+    assert L.hip_graph_begin() == 0
+    A.PagedAttentionImpl.execute(0, node)
+    g = L.hip_graph_end()
+    assert g
+    try:
+        for i in range(3):
+            node_out.fill_(float("nan"))
+            junk = torch.randn(1 << 20, device="cuda").sum()  # eager work between the replays
+            torch.cuda.synchronize()
+            L.hip_graph_launch(g)
+            torch.cuda.synchronize()
+            check_hip_error(f"pieces replay {i}")
+            np.testing.assert_array_equal(to_u16(node_out), ref)
+            del junk
+    finally:
+        L.hip_graph_destroy(g)
