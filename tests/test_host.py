@@ -212,3 +212,26 @@ def test_bench_kernel_names_follow_the_header():
     assert set(bench.PREFILL_KERNELS) == vals
     assert "split" in bench.PREFILL_KERNELS[int(re.search(r"LLMGEN_PREFILL_SPLIT\s*=\s*(\d+)", hdr).group(1))]
     assert "mixed" in bench.PREFILL_KERNELS[int(re.search(r"LLMGEN_PREFILL_MIXED\s*=\s*(\d+)", hdr).group(1))]
+
+
+def test_prefill_plan_rules():
+    """hip_attn_prefill_plan's choice is integer arithmetic on the step's shape and the CU count (256 without a GPU,
+    as on MI355X): pure prefill steps of at most half a two-head unit per CU (one one-head unit at GQA 1) take the
+    pieces kernel, up to 2.5 units per CU the key split, c3's 792 units the heavy-tile split, c5p's GQA 4 the 8-wave
+    kernel; mixed steps with a known count the mixed-step kernel at GQA 2 / 4, else (few prefill units) the pieces
+    kernel beside the decode-row launch; an unknown count the 4-wave kernel beside the decode-row launch."""
+    from llmgen_amd._lib import lib
+
+    L = lib()
+    MIXED, KEYSPLIT, W2, W4, W8, SPLIT, PIECES, ROWS = 1, 2, 3, 4, 5, 6, 7, 16
+    plan = lambda n, nq, nkv, rows: L.hip_attn_prefill_plan(n, nq, nkv, 128, 256, rows)  # noqa: E731
+    assert plan(8, 16, 8, 0) == PIECES and plan(16, 16, 8, 0) == PIECES
+    assert plan(17, 16, 8, 0) == KEYSPLIT and plan(80, 16, 8, 0) == KEYSPLIT
+    assert plan(99, 16, 8, 0) == SPLIT
+    assert plan(256, 32, 8, 0) == W8
+    assert plan(16, 16, 16, 0) == PIECES and plan(17, 16, 16, 0) == W2
+    assert plan(71, 16, 8, 63) == MIXED and plan(71, 32, 8, 63) == MIXED
+    assert plan(71, 16, 16, 63) == PIECES | ROWS and plan(71, 64, 8, 67) == PIECES | ROWS
+    assert plan(400, 16, 16, 63) == W2 | ROWS
+    assert plan(8, 16, 8, -1) == W4 | ROWS
+    assert plan(0, 16, 8, 0) == 0 and plan(4, 24, 8, 0) == -1
