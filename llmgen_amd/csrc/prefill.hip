@@ -147,7 +147,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
     const int tile = n_tiles - 1 - t;
     const int s = tile_seq[tile], q_len = cu_q[s + 1] - cu_q[s], ctx = ctx_lens[s];
     const int n = q_len > 1 && ctx >= q_len ? (ctx - q_len + min(tile_q0[tile] + BQ, q_len) + BK - 1) / BK : 0;
-    if (n < 2) {  // nothing to split (a one-tile unit, a padding or single-row segment): the first half runs it
+    if (n < 4) {  // not worth a merge (a unit under four key tiles, a padding or single-row segment): the first
+                  // half runs it whole (64 prompts of 128 tokens: 37.1 -> 35.2 us)
         if (half == 0) body(bid, 0, -1, nullptr);
         return;
     }
