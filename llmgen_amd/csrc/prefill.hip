@@ -168,17 +168,20 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
     if (threadIdx.x == 0) __hip_atomic_store(counters + bid, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// ---- pure prefill of few units: each unit's key tiles over several workgroups ----
+// ---- prefill of few units: each unit's key tiles over several workgroups ----
 //
-// A pure prefill step of at most CUs / 2 units (tile x KV head x head pair; CUs one-head units at G = 1) -- a chunk of a long prompt against its
-// cached keys, a short prompt -- leaves most of the chip idle with one workgroup per unit: a 512-row chunk at
-// GQA 2 against 32K cached keys is 64 units of 520 key tiles, one chain each on 64 of 256 CUs (460 us).  Here each
-// unit gets P workgroups (P = min(8, 2 CUs / units), so all are resident at once); a unit of n key tiles uses
-// min(P, ceil(n / 4)) of them, each a contiguous equal share of its key tiles, and the others exit.  A unit with
-// one piece stores its rows directly; otherwise every piece leaves its partial (O, m, l) in the library's scratch
-// array (shared with the heavy-tile split) and the last to finish, by a ticket on a per-unit counter, merges them
-// in piece order, so the output is bit-reproducible.  The unit index runs fastest in the grid, so a KV head's
-// workgroups stay on one XCD.
+// A pure prefill step of few units -- a chunk of a long prompt against its cached keys, a short prompt -- leaves
+// most of the chip idle with one workgroup per unit: a 512-row chunk at GQA 2 against 32K cached keys is 64 units
+// of 520 key tiles, one chain each on 64 of 256 CUs (455 us).  Units are (tile x KV head x head pair) for 4-wave
+// workgroups, or (tile x head) for 2-wave ones at G = 1; a step qualifies with at most half a 4-wave unit (one
+// 2-wave unit) per CU.  Each unit gets P workgroups (P = min(8, the CUs' workgroup slots / units), so all are
+// resident at once); a unit of n key tiles uses min(P, ceil(n / 4)) of them, each a contiguous equal share of its
+// key tiles, and the others exit.  A unit with one piece stores its rows directly; otherwise every piece leaves
+// its partial (O, m, l) in the library's scratch array (shared with the heavy-tile split) and the last to finish,
+// by a ticket on a per-unit counter, merges them in piece order, so the output is bit-reproducible.  The unit
+// index runs fastest in the grid, so a KV head's workgroups stay on one XCD.  A mixed step at G = 1, 8 or 16 runs
+// its prefill tiles here beside the decode-row launch: the list's leading single-row tiles (n_front) get one
+// workgroup per unit and are not split.
 constexpr int PIECES_MAX = 8, PIECE_MIN_TILES = 4;
 
 template <int MODE, int NW>
