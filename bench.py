@@ -345,7 +345,7 @@ def main() -> int:
 
     extra = {}
     if not args.no_extra:
-        for name in ("c1", "c5d", "c3", "c5p", "c4"):
+        for name in ("c1", "c5d", "c3", "c5p", "c4", "chunk32k", "chunkmix"):
             try:
                 extra[name] = bench_extra(name, iters=20 if name != "c5p" else 5)
             except Exception as e:  # report, keep the headline line

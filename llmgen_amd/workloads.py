@@ -12,6 +12,8 @@ Configurations (shape Qwen3-0.6B unless stated: 16 Q heads, 8 KV heads, head_dim
   c4  mixed step: 256 sequences with ctx ~ U[100, 2048]; 8 prefill a 512-token chunk, 248 decode one token
   c5d decode, 32 Q / 8 KV heads (GQA 4), 16 sequences at ctx 32768, permuted blocks, std 1
   c5p prefill, 32 Q / 8 KV heads, one 16384-token causal prompt, permuted blocks, std 1
+Outside BASELINE, ``chunk32k`` (one 512-row chunk against 32256 cached keys) and ``chunkmix`` (a 512-row chunk on
+16384 keys beside 63 decode rows) are chunked-prefill steps of few, long units.
 Reference test cases (src/backend/cuda/kernel_test.zig:151-232, src/backend/cpu/attention.zig:188-251) are
 ``kt_prefill``, ``kt_decode`` and ``cpu_mixed``, with U(-1, 1) inputs from a seeded generator.  Further small
 steps cover other GQA group sizes (``gqa*``), block sizes 48 and 6 (``bs48*``, ``bs6*``) and G = 1 at block sizes 6
@@ -200,6 +202,21 @@ def make(name: str, seed: Optional[int] = None) -> Workload:
         tables, nb = _tables(rng, lens, bs, permute=True)
         return Workload("c5p", 32, 8, 128, bs, nb, 64, 32768, [Entry(0, 16384, tables[0])], std=1.0, seed=s,
                         note="causal prefill GQA4 T=16384 permuted blocks")
+    # ---- chunked prefill against a long cached context (outside BASELINE: the pieces kernels' case) ----
+    if name == "chunk32k":
+        s = 8 if seed is None else seed
+        rng = np.random.default_rng(s)
+        tables, nb = _tables(rng, [32768], bs, permute=True)
+        return Workload("chunk32k", 16, 8, 128, bs, nb, 128, 32768, [Entry(32256, 512, tables[0])], std=1.0, seed=s,
+                        decode=False, note="512-row chunk of a 32768-token prompt, 32256 keys cached")
+    if name == "chunkmix":
+        s = 9 if seed is None else seed
+        rng = np.random.default_rng(s)
+        dctx = [int(x) for x in rng.integers(1024, 3073, size=63)]
+        tables, nb = _tables(rng, [16384] + dctx, bs, permute=True)
+        ents = [Entry(15872, 512, tables[0])] + [Entry(c - 1, 1, t) for c, t in zip(dctx, tables[1:])]
+        return Workload("chunkmix", 16, 8, 128, bs, nb, 64, 16384, ents, std=1.0, seed=s, decode=False,
+                        note="512-row chunk on 16384 keys + 63 decodes, ctx~U[1024,3072]")
     # ---- reference test cases ----
     if name in ("kt_prefill", "kt_decode"):
         # kernel_test.zig:151-232: nq=4, nkv=2, hd=128, bs=16, 32 blocks, ctx=150, bt[i]=(i*7+3)%32 (16 columns)
