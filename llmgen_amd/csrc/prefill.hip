@@ -180,8 +180,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 // its partial (O, m, l) in the library's scratch array (shared with the heavy-tile split) and the last to finish,
 // by a ticket on a per-unit counter, merges them in piece order, so the output is bit-reproducible.  The unit
 // index runs fastest in the grid, so a KV head's workgroups stay on one XCD.  A mixed step at G = 1, 8 or 16 runs
-// its prefill tiles here beside the decode-row launch: the list's leading single-row tiles (n_front) get one
-// workgroup per unit and are not split.
+// its prefill tiles here beside the decode-row launch: the list's leading single-row tiles (n_front) are only
+// checked, a few hundred units per workgroup, and not split.
 constexpr int PIECES_MAX = 8, PIECE_MIN_TILES = 4;
 
 template <int MODE, int NW>
@@ -196,14 +196,29 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)
     __shared__ __attribute__((aligned(16))) unsigned char lds[sizeof(PrefillLds<NW, 1>)];
     __shared__ int s_last;
     constexpr int PSTRIDE = NW * PART_WAVE_FLOATS;  // scratch floats per piece
-    // The list's first n_front tiles (a mixed step's single-row segments) get one workgroup per unit, which runs a
-    // multi-row tile found there whole and skips the single rows (the decode-row launch streams them); the rest of
-    // the list is split into pieces.
-    const long front_wg = (long)n_front * nkv * head_groups;
+    // The list's first n_front tiles (a mixed step's single-row segments, streamed by the decode-row launch) are
+    // checked 64 * NW units per workgroup, one per thread; a multi-row tile found there (a list out of order) runs
+    // whole.  The rest of the list is split into pieces.
+    constexpr int FRONT = 64 * NW;
+    const long front_units = (long)n_front * nkv * head_groups;
+    const long front_wg = (front_units + FRONT - 1) / FRONT;
     if (blockIdx.x < front_wg) {
-        prefill_body<NW, MODE, 1, true>(out, q, kc, vc, block_tables, ctx_lens, cu_q, tile_seq, tile_q0, n_front, nq,
-                                        nkv, G, head_groups, max_blocks, block_size, bs_shift, scale_log2,
-                                        (int)blockIdx.x, lds, 0, -1, nullptr);
+        __shared__ int s_multi[FRONT];
+        const long u = (long)blockIdx.x * FRONT + threadIdx.x;
+        int multi = 0;
+        if (u < front_units) {
+            const int s = tile_seq[n_front - 1 - (int)(u / (nkv * head_groups))];
+            multi = cu_q[s + 1] - cu_q[s] > 1;
+        }
+        s_multi[threadIdx.x] = multi;
+        __syncthreads();
+        for (int i = 0; i < FRONT; ++i) {
+            if (!s_multi[i]) continue;  // uniform: every thread reads the same flag
+            prefill_body<NW, MODE, 1, true>(out, q, kc, vc, block_tables, ctx_lens, cu_q, tile_seq, tile_q0, n_front,
+                                            nq, nkv, G, head_groups, max_blocks, block_size, bs_shift, scale_log2,
+                                            (int)((long)blockIdx.x * FRONT + i), lds, 0, -1, nullptr);
+            __syncthreads();  // the next unit reuses the LDS stages
+        }
         return;
     }
     tile_seq += n_front;
@@ -316,7 +331,7 @@ bool launch_prefill_pieces(int mode, bf16_t *out, const bf16_t *q, const bf16_t 
     const int nw = G == 1 ? 2 : 4;  // one head per 2-wave workgroup at G = 1, else two per 4-wave workgroup
     const int head_groups = G / (nw / 2);
     const long units = (long)(n_tiles - n_front) * nkv * head_groups;
-    const long front_wg = (long)n_front * nkv * head_groups;
+    const long front_wg = ((long)n_front * nkv * head_groups + 64 * nw - 1) / (64 * nw);  // as the kernel counts
     const int P = prefill_pieces(units, nw);
     if (P <= 0) return false;
     float *part = reinterpret_cast<float *>(symbol_address(HIP_SYMBOL(g_split_part)));

@@ -143,3 +143,46 @@ def test_pieces_prefill_graph_replay(gpu):
             del junk
     finally:
         L.hip_graph_destroy(g)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", ["gqa8", "gqa1"])
+def test_pieces_beside_rows_any_tile_order(gpu, name):
+    """A mixed step at GQA 8 / 1 with a known single-row count runs its prefill tiles in the pieces kernel beside the
+    decode-row launch, expecting the single rows first; a seeded shuffle of the tile list (multi-row tiles among
+    the leading single-row part, single rows among the rest) must still give every row: against the oracle."""
+    from harness import check_hip_error
+    from llmgen_amd.workloads import make
+    import oracle
+
+    wl = make(name)
+    print(f"[gpu-test] pieces any order {name}", flush=True)
+    t = wl.tensors(device="cuda")
+    L = lib()
+    meta = wl.meta(L.hip_attn_prefill_tile())
+    assert not meta.decode and meta.single_rows() > 0
+    if torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        assert L.hip_attn_prefill_plan(meta.n_tiles, wl.nq, wl.nkv, wl.hd, wl.block_size, meta.single_rows()) == \
+            PIECES | 16
+    kc, vc = t["kc"].clone(), t["vc"].clone()
+    buf = meta.packed().copy()
+    perm = np.random.default_rng(9).permutation(meta.n_tiles)
+    o_s, o_q = meta.offsets["tile_seq"], meta.offsets["tile_q0"]
+    buf[o_s:o_s + meta.n_tiles] = meta.tile_seq[perm]
+    buf[o_q:o_q + meta.n_tiles] = meta.tile_q0[perm]
+    moved = np.diff(meta.cu_q)[meta.tile_seq[perm]][:meta.single_rows()]
+    assert (moved > 1).any(), "the shuffle must put multi-row tiles into the leading part"
+    seg = torch.from_numpy(buf).to("cuda")
+    off = {k: seg.data_ptr() + 4 * v for k, v in meta.offsets.items()}
+    L.hip_store_kv(t["k"].data_ptr(), t["v"].data_ptr(), off["slots"], kc.data_ptr(), vc.data_ptr(), wl.n_tok,
+                   wl.nkv, wl.hd, wl.block_size)
+    out = torch.full((wl.n_tok, wl.nq, wl.hd), float("nan"), dtype=torch.bfloat16, device="cuda")
+    L.hip_attn_prefill_rows(out.data_ptr(), t["q"].data_ptr(), kc.data_ptr(), vc.data_ptr(), off["block_tables"],
+                            off["ctx"], off["cu_q"], off["tile_seq"], off["tile_q0"], meta.n_tiles, wl.nq, wl.nkv,
+                            wl.hd, wl.max_blocks, wl.block_size, wl.scale, meta.single_rows())
+    torch.cuda.synchronize()
+    check_hip_error(f"{name} shuffled")
+    got = to_u16(out)
+    assert not np.isnan(oracle.bf16_to_f32(got)).any()
+    _, _, _, of = run_oracle(wl, t)
+    compare(got, of, f"{name} shuffled")
